@@ -1,0 +1,426 @@
+/* Flash attention forward for gfx950, head_dim 128, non-causal, bf16 in/out
+ * with an F32 online softmax: joint self-attention (q_rows == kv_rows) and
+ * cross attention (q_rows != kv_rows) share one kernel.
+ *
+ * Reference semantics (h3_cuda_attention.cu:1508-1812): scores scaled by
+ * `scale`, exp2-domain softmax with scale*log2(e) folded in, running max and
+ * sum in F32, P rounded to bf16 (RNE) before P.V, the sum taken over the
+ * unrounded P, output = O / l rounded to bf16, keys past the end masked.
+ *
+ * MI355X design (not the reference's warp tiling):
+ *   - the score tile is computed transposed, S^T = K . Q^T, with
+ *     v_mfma_f32_32x32x16_bf16: K fragments come from LDS, Q fragments stay
+ *     in registers for the whole key loop.  Each lane then owns one query
+ *     column and 16 keys of it, so the row max / row sum are in-lane
+ *     reductions plus a single exchange with the lane 32 away;
+ *   - O^T = V^T . P^T: the P^T operand is the S^T accumulator itself, packed
+ *     to bf16 in place.  The accumulator's key order inside a lane is
+ *     {4h..4h+3, 8+4h..8+4h+3, ...}; the V^T operand is read in exactly that
+ *     key order (two 8-byte LDS reads), so P never goes through LDS;
+ *   - V is transposed once per tile while being staged into LDS
+ *     (V^T rows of 64 keys, 136-byte pitch), K is staged row-major with an
+ *     XOR swizzle on 16-byte chunks;
+ *   - 4 wave64s x 64 queries = 256 queries per workgroup, 64-key tiles,
+ *     double-buffered LDS (2 x 33 KiB) with the next tile's global loads in
+ *     flight during the current tile's 64 MFMAs per wave;
+ *   - the grid is 1-D and regrouped per XCD so the query blocks of one head
+ *     run on one XCD and share its L2 copy of that head's K and V.
+ *
+ * A two-pass reference kernel (the reference's naive SDPA,
+ * h3_cuda_attention.cu:488-549: one workgroup per (row, head), normalised
+ * F32 probabilities) serves other head sizes and H3_HIP_REFERENCE=1.
+ */
+#include "hk_common.h"
+#include "hk_internal.h"
+
+#include <math.h>
+
+#define HK_HD 128
+#define HK_QB 256             /* queries per workgroup */
+#define HK_KT 64              /* keys per tile */
+#define HK_K_BYTES (HK_KT * HK_HD * 2)        /* 16 KiB, 256-B rows */
+#define HK_VT_PITCH 136                        /* bytes per V^T row */
+#define HK_VT_BYTES (HK_HD * HK_VT_PITCH)      /* 17 KiB */
+#define HK_STAGE_BYTES (HK_K_BYTES + HK_VT_BYTES)
+#define HK_ATTN_LDS (2 * HK_STAGE_BYTES)
+
+typedef int hk_v4i __attribute__((ext_vector_type(4)));
+typedef int hk_v2i __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t hk_attn_rsrc(
+    const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base),
+                                             (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+/* K tile: row = key (256 B), 16 chunks, chunk ^= row & 15 */
+__device__ __forceinline__ uint32_t hk_k_swz(uint32_t row, uint32_t chunk) {
+    return row * 256u + ((chunk ^ (row & 15u)) << 4);
+}
+
+struct hk_attn_args {
+    const uint16_t *q, *k, *v;
+    uint16_t *o;
+    uint32_t q_rows, kv_rows, heads, q_blocks;
+    uint32_t q_bytes, kv_bytes;
+    float scale_log2;
+    int head_major;
+};
+
+__global__ void __launch_bounds__(256, 1) hk_flash_fwd(hk_attn_args a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t hk_lds[];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t col = lane & 31u, half = lane >> 5;
+
+    uint32_t pid = blockIdx.x;
+    const uint32_t nwg = gridDim.x;
+    if ((nwg & 7u) == 0) pid = (pid & 7u) * (nwg >> 3) + (pid >> 3);
+    const uint32_t qblock = pid % a.q_blocks, head = pid / a.q_blocks;
+    const uint32_t row_stride = a.heads * HK_HD; /* elements */
+
+    const __amdgpu_buffer_rsrc_t qr = hk_attn_rsrc(a.q, a.q_bytes);
+    const __amdgpu_buffer_rsrc_t kr = hk_attn_rsrc(a.k, a.kv_bytes);
+    const __amdgpu_buffer_rsrc_t vr = hk_attn_rsrc(a.v, a.kv_bytes);
+
+    /* ---- Q fragments: B operand of S^T = K . Q^T ----
+     * group g, k-step ks: Q[q][16 ks + 8 half .. +8] */
+    const uint32_t qbase = qblock * HK_QB + wave * 64u;
+    hk_bf16x8 qf[2][8];
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+        const uint32_t q = qbase + g * 32u + col;
+        const uint32_t off = q < a.q_rows
+            ? ((q * row_stride + head * HK_HD + half * 8u) * 2u)
+            : 0xfffffff0u;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            hk_v4i raw = __builtin_amdgcn_raw_buffer_load_b128(
+                qr, off == 0xfffffff0u ? off : off + ks * 32u, 0, 0);
+            qf[g][ks] = __builtin_bit_cast(hk_bf16x8, raw);
+        }
+    }
+
+    /* ---- staging plan ----
+     * K: thread t loads chunk (t & 15) of key rows (t >> 4) + 16 i
+     * V: thread t loads chunk dc = t & 15 of key rows 4 kg .. 4 kg + 3,
+     *    kg = t >> 4, and writes them transposed */
+    const uint32_t sc = tid & 15u, sr = tid >> 4;
+    hk_v4i kreg[4], vreg[4];
+    auto load_tile = [&](uint32_t kv0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t krow = kv0 + sr + 16u * i;
+            const uint32_t koff = krow < a.kv_rows
+                ? ((krow * row_stride + head * HK_HD + sc * 8u) * 2u)
+                : 0xfffffff0u;
+            kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 0, 0);
+            const uint32_t vrow = kv0 + sr * 4u + i;
+            const uint32_t voff = vrow < a.kv_rows
+                ? ((vrow * row_stride + head * HK_HD + sc * 8u) * 2u)
+                : 0xfffffff0u;
+            vreg[i] = __builtin_amdgcn_raw_buffer_load_b128(vr, voff, 0, 0);
+        }
+    };
+    auto store_tile = [&](uint32_t stage) {
+        uint8_t *ks = hk_lds + stage * HK_STAGE_BYTES;
+        uint8_t *vt = ks + HK_K_BYTES;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            *(hk_v4i *)(ks + hk_k_swz(sr + 16u * i, sc)) = kreg[i];
+        /* transpose 4 keys x 8 dims -> 8 rows of 4 keys */
+        const uint16_t *v16[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) v16[i] = (const uint16_t *)&vreg[i];
+#pragma unroll
+        for (int d = 0; d < 8; d++) {
+            uint2 packed;
+            packed.x = (uint32_t)v16[0][d] | ((uint32_t)v16[1][d] << 16);
+            packed.y = (uint32_t)v16[2][d] | ((uint32_t)v16[3][d] << 16);
+            *(uint2 *)(vt + (sc * 8u + d) * HK_VT_PITCH + sr * 8u) = packed;
+        }
+    };
+
+    hk_f32x16 o[4][2];
+#pragma unroll
+    for (int d = 0; d < 4; d++)
+#pragma unroll
+        for (int g = 0; g < 2; g++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) o[d][g][r] = 0.0f;
+    float m_run[2] = {-INFINITY, -INFINITY};
+    float l_part[2] = {0.0f, 0.0f};
+
+    const uint32_t tiles = (a.kv_rows + HK_KT - 1) / HK_KT;
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+
+    for (uint32_t t = 0; t < tiles; t++) {
+        const uint32_t stage = t & 1u;
+        if (t + 1 < tiles) load_tile((t + 1) * HK_KT);
+        const uint8_t *ks = hk_lds + stage * HK_STAGE_BYTES;
+        const uint8_t *vt = ks + HK_K_BYTES;
+
+        /* S^T[kt][g]: keys kt*32 + .., queries g*32 + col */
+        hk_f32x16 s[2][2];
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+            for (int g = 0; g < 2; g++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) s[kt][g][r] = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) {
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++) {
+                hk_bf16x8 kf = *(const hk_bf16x8 *)(
+                    ks + hk_k_swz(kt * 32u + col, kk * 2u + half));
+#pragma unroll
+                for (int g = 0; g < 2; g++)
+                    s[kt][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        kf, qf[g][kk], s[kt][g], 0, 0, 0);
+            }
+        }
+
+        /* online softmax per query column */
+        const uint32_t kv0 = t * HK_KT;
+        const bool tail = kv0 + HK_KT > a.kv_rows;
+        hk_bf16x8 pf[2][2][2]; /* [kt][step][g] */
+#pragma unroll
+        for (int g = 0; g < 2; g++) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    float v = s[kt][g][r] * a.scale_log2;
+                    if (tail) {
+                        const uint32_t key = kv0 + kt * 32u + (r >> 2) * 8u +
+                                             half * 4u + (r & 3);
+                        if (key >= a.kv_rows) v = -INFINITY;
+                    }
+                    s[kt][g][r] = v;
+                    mx = fmaxf(mx, v);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float m_new = fmaxf(m_run[g], mx);
+            const float ref = m_new == -INFINITY ? 0.0f : m_new;
+            const float c = __builtin_amdgcn_exp2f(m_run[g] - ref);
+            m_run[g] = m_new;
+            float sum = 0.0f;
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++) {
+                float p[16];
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    p[r] = __builtin_amdgcn_exp2f(s[kt][g][r] - ref);
+                    sum += p[r];
+                }
+#pragma unroll
+                for (int st = 0; st < 2; st++) {
+                    hk_bf16x8 v;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[e] = (__bf16)p[st * 8 + e];
+                    pf[kt][st][g] = v;
+                }
+            }
+            l_part[g] = l_part[g] * c + sum;
+#pragma unroll
+            for (int d = 0; d < 4; d++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) o[d][g][r] *= c;
+        }
+
+        /* O^T[d][g] += V^T[d, keys] . P^T[keys, g] */
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+            for (int st = 0; st < 2; st++) {
+                const uint32_t key = kt * 32u + st * 16u + half * 4u;
+#pragma unroll
+                for (int d = 0; d < 4; d++) {
+                    const uint8_t *row = vt + (d * 32u + col) * HK_VT_PITCH;
+                    hk_v2i lo = *(const hk_v2i *)(row + key * 2u);
+                    hk_v2i hi = *(const hk_v2i *)(row + (key + 8u) * 2u);
+                    hk_v4i both = {lo[0], lo[1], hi[0], hi[1]};
+                    hk_bf16x8 vf = __builtin_bit_cast(hk_bf16x8, both);
+#pragma unroll
+                    for (int g = 0; g < 2; g++)
+                        o[d][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                            vf, pf[kt][st][g], o[d][g], 0, 0, 0);
+                }
+            }
+
+        if (t + 1 < tiles) store_tile(stage ^ 1u);
+        __syncthreads();
+    }
+
+    /* ---- normalise and store: lane owns query column `col` of group g and
+     * dims d*32 + (r/4)*8 + 4*half + r%4 */
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+        const float l = l_part[g] + __shfl_xor(l_part[g], 32, 64);
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        const uint32_t q = qbase + g * 32u + col;
+        if (q >= a.q_rows) continue;
+        uint16_t *out = a.head_major
+            ? a.o + ((size_t)head * a.q_rows + q) * HK_HD
+            : a.o + (size_t)q * row_stride + (size_t)head * HK_HD;
+#pragma unroll
+        for (int d = 0; d < 4; d++)
+#pragma unroll
+            for (int blk = 0; blk < 4; blk++) {
+                const uint32_t dim = d * 32u + blk * 8u + half * 4u;
+                uint2 packed = {
+                    hk_pack2(o[d][g][blk * 4 + 0] * inv,
+                             o[d][g][blk * 4 + 1] * inv),
+                    hk_pack2(o[d][g][blk * 4 + 2] * inv,
+                             o[d][g][blk * 4 + 3] * inv)};
+                *(uint2 *)(out + dim) = packed;
+            }
+    }
+}
+
+/* Two-pass reference: one workgroup per (query row, head); scores in LDS. */
+__global__ void __launch_bounds__(256)
+hk_attn_reference(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                  uint16_t *o, uint32_t q_rows, uint32_t kv_rows,
+                  uint32_t heads, uint32_t head_dim, float scale,
+                  int head_major) {
+    extern __shared__ float scores[];
+    __shared__ float scratch[16];
+    const uint32_t row = blockIdx.x, head = blockIdx.y;
+    const size_t q_base = ((size_t)row * heads + head) * head_dim;
+    float local_max = -INFINITY;
+    for (uint32_t key = threadIdx.x; key < kv_rows; key += blockDim.x) {
+        const size_t k_base = ((size_t)key * heads + head) * head_dim;
+        float dot = 0.0f;
+        for (uint32_t d = 0; d < head_dim; d++)
+            dot = fmaf(hk_bf2f(q[q_base + d]), hk_bf2f(k[k_base + d]), dot);
+        dot *= scale;
+        scores[key] = dot;
+        local_max = fmaxf(local_max, dot);
+    }
+    /* block max through the sum helper's pattern */
+    local_max = hk_wave_max(local_max);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = local_max;
+    __syncthreads();
+    float maximum = -INFINITY;
+    for (uint32_t w = 0; w < (blockDim.x >> 6); w++)
+        maximum = fmaxf(maximum, scratch[w]);
+    float local_sum = 0.0f;
+    for (uint32_t key = threadIdx.x; key < kv_rows; key += blockDim.x) {
+        float p = expf(scores[key] - maximum);
+        scores[key] = p;
+        local_sum += p;
+    }
+    const float inverse = 1.0f / hk_block_sum(local_sum, scratch);
+    for (uint32_t d = threadIdx.x; d < head_dim; d += blockDim.x) {
+        float sum = 0.0f;
+        for (uint32_t key = 0; key < kv_rows; key++)
+            sum = fmaf(scores[key] * inverse,
+                       hk_bf2f(v[((size_t)key * heads + head) * head_dim + d]),
+                       sum);
+        const size_t out = head_major
+            ? ((size_t)head * q_rows + row) * head_dim + d
+            : q_base + d;
+        o[out] = hk_f2bf(sum);
+    }
+}
+
+static bool hk_attn_lds_ready = false;
+
+int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
+                      const uint16_t *k, const uint16_t *v, uint16_t *o,
+                      uint32_t q_rows, uint32_t kv_rows, uint32_t heads,
+                      uint32_t head_dim, float scale, int head_major) {
+    if (!q_rows || !heads) return 1;
+    const uint64_t q_bytes = (uint64_t)q_rows * heads * head_dim * 2;
+    const uint64_t kv_bytes = (uint64_t)kv_rows * heads * head_dim * 2;
+    const bool flash = !gpu->reference_kernels && head_dim == HK_HD &&
+                       kv_rows > 0 && q_bytes < 0xfffff000ull &&
+                       kv_bytes < 0xfffff000ull &&
+                       ((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0 &&
+                       ((uintptr_t)v & 15) == 0 && ((uintptr_t)o & 7) == 0;
+    if (flash) {
+        if (!hk_attn_lds_ready) {
+            (void)hipFuncSetAttribute((const void *)hk_flash_fwd,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      HK_ATTN_LDS);
+            hk_attn_lds_ready = true;
+        }
+        hk_attn_args a;
+        a.q = q; a.k = k; a.v = v; a.o = o;
+        a.q_rows = q_rows; a.kv_rows = kv_rows; a.heads = heads;
+        a.q_blocks = (q_rows + HK_QB - 1) / HK_QB;
+        a.q_bytes = (uint32_t)q_bytes;
+        a.kv_bytes = (uint32_t)kv_bytes;
+        a.scale_log2 = scale * 1.4426950408889634f;
+        a.head_major = head_major;
+        hipLaunchKernelGGL(hk_flash_fwd, dim3(a.q_blocks * heads), dim3(256),
+                           HK_ATTN_LDS, gpu->stream, a);
+        return 1;
+    }
+    if ((size_t)kv_rows * sizeof(float) > 64 * 1024)
+        return hk_fail(gpu, "reference attention supports at most 16384 keys");
+    hipLaunchKernelGGL(hk_attn_reference, dim3(q_rows, heads), dim3(256),
+                       (size_t)(kv_rows ? kv_rows : 1) * sizeof(float),
+                       gpu->stream, q, k, v, o, q_rows, kv_rows, heads,
+                       head_dim, scale, head_major);
+    return 1;
+}
+
+extern "C" {
+
+static int hk_sdpa(h3_gpu *gpu, h3_gpu_tensor *output,
+                   const h3_gpu_tensor *query, const h3_gpu_tensor *key,
+                   const h3_gpu_tensor *value, uint32_t q_rows,
+                   uint32_t kv_rows, uint32_t heads, uint32_t head_dim,
+                   float scale, int head_major, const char *name) {
+    size_t q_count = (size_t)q_rows * heads * head_dim;
+    size_t kv_count = (size_t)kv_rows * heads * head_dim;
+    if (!hk_require(gpu, query, q_count, H3_GPU_BF16, "SDPA query") ||
+        !hk_require(gpu, key, kv_count, H3_GPU_BF16, "SDPA key") ||
+        !hk_require(gpu, value, kv_count, H3_GPU_BF16, "SDPA value") ||
+        !hk_require(gpu, output, q_count, H3_GPU_BF16, "SDPA output") ||
+        !hk_require_active(gpu))
+        return 0;
+    hk_op_begin(gpu, name);
+    if (!hk_attention_bf16(gpu, HK_CBF16(query), HK_CBF16(key),
+                           HK_CBF16(value), HK_BF16(output), q_rows, kv_rows,
+                           heads, head_dim, scale, head_major))
+        return 0;
+    return hk_op_end(gpu, name, HK_KIND_SDPA);
+}
+
+int h3_gpu_sdpa_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                     const h3_gpu_tensor *query, const h3_gpu_tensor *key,
+                     const h3_gpu_tensor *value, uint32_t sequence,
+                     uint32_t heads, uint32_t head_dim, float scale) {
+    return hk_sdpa(gpu, output, query, key, value, sequence, sequence, heads,
+                   head_dim, scale, 0, "attention");
+}
+
+int h3_gpu_sdpa_bf16_head_major_output(h3_gpu *gpu, h3_gpu_tensor *output,
+                                       const h3_gpu_tensor *query,
+                                       const h3_gpu_tensor *key,
+                                       const h3_gpu_tensor *value,
+                                       uint32_t sequence, uint32_t heads,
+                                       uint32_t head_dim, float scale) {
+    return hk_sdpa(gpu, output, query, key, value, sequence, sequence, heads,
+                   head_dim, scale, 1, "attention");
+}
+
+int h3_gpu_sdpa_cross_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                           const h3_gpu_tensor *query,
+                           const h3_gpu_tensor *key,
+                           const h3_gpu_tensor *value, uint32_t q_rows,
+                           uint32_t kv_rows, uint32_t heads,
+                           uint32_t head_dim, float scale) {
+    return hk_sdpa(gpu, output, query, key, value, q_rows, kv_rows, heads,
+                   head_dim, scale, 0, "attention_cross");
+}
+
+} /* extern "C" */

@@ -1,0 +1,499 @@
+/* BF16 GEMM for gfx950: C[M,N] = epilogue(X[M,K] . W[N,K]^T (+ bias)).
+ *
+ * Both operands are K-contiguous (activations row-major, weights in the
+ * checkpoint's [out, in] order), which is the natural operand order of the
+ * CDNA matrix cores: every MFMA operand fragment is 8 consecutive k values
+ * of one row, i.e. one 16-byte LDS read per lane.
+ *
+ * Tiling (per 256-thread workgroup, one workgroup per CU at a time):
+ *   - 256 (W rows) x 256 (X rows) output tile, K step 64;
+ *   - four wave64s in a 2x2 grid, each owning a 128x128 sub-tile held as
+ *     4x4 accumulators of v_mfma_f32_32x32x16_bf16 (256 f32 per lane);
+ *   - X and W tiles staged through LDS with raw buffer loads (16 B per
+ *     lane; rows past M read as zero through the buffer bound), double
+ *     buffered: the next K step's global loads are in flight while the
+ *     current step's 64 MFMAs per wave run;
+ *   - LDS rows are 128 B (64 bf16); 16-byte chunks are XOR-swizzled with the
+ *     row index so that the 32 rows a fragment read touches fall on
+ *     distinct banks;
+ *   - the MFMA computes D = W_tile . X_tile^T, so each lane's accumulator
+ *     holds 4 consecutive output columns of one output row: the epilogue
+ *     writes 8-byte packed bf16 groups;
+ *   - the workgroup -> tile order is XCD-aware: consecutive workgroups are
+ *     dealt round-robin to the 8 XCDs, so workgroup ids are first regrouped
+ *     per XCD and then walked in GROUP_M-tall column bands, keeping the
+ *     tiles that share W (and X) rows inside one XCD's L2.
+ *
+ * Epilogues: plain store (+bias), SwiGLU (the tile's W rows interleave 64
+ * gate and 64 up rows per wave so each lane holds matching gate/up values;
+ * activation bf16(silu(bf16 g) * bf16 u), the reference's rounding,
+ * h3_cuda_core.cu:104-114 fed by a bf16 fc1 output, :1067-1104), GELU-tanh.
+ *
+ * A sequential-k reference kernel (one thread per output, fmaf from the
+ * bias, bf16 inputs: the reference's hand kernel h3_cuda_core.cu:358-371)
+ * serves shapes the MFMA path does not take and H3_HIP_REFERENCE=1.
+ */
+#include "hk_common.h"
+#include "hk_internal.h"
+
+#include <math.h>
+
+#define HK_BM 256
+#define HK_BN 256
+#define HK_BK 64
+#define HK_GEMM_THREADS 256
+#define HK_TILE_BYTES (HK_BM * HK_BK * 2) /* 32 KiB per operand per stage */
+#define HK_GEMM_LDS (4 * HK_TILE_BYTES)   /* 2 stages x 2 operands */
+#define HK_GROUP_M 8
+
+typedef int hk_v4i __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t hk_rsrc(const void *base,
+                                                          uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base),
+                                             (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+/* byte offset of 16-byte chunk `chunk` of LDS row `row` */
+__device__ __forceinline__ uint32_t hk_swz(uint32_t row, uint32_t chunk) {
+    return row * 128u + ((chunk ^ (row & 7u)) << 4);
+}
+
+__device__ __forceinline__ float hk_silu_f(float x) {
+    return x / (1.0f + expf(-x));
+}
+
+__device__ __forceinline__ float hk_gelu_tanh_f(float x) {
+    float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+    return inner <= -10.0f ? 0.0f
+         : inner >= 10.0f  ? x
+                           : 0.5f * x * (1.0f + tanhf(inner));
+}
+
+struct hk_gemm_args {
+    const uint16_t *x;     /* [M, K] */
+    const uint16_t *w;     /* [W rows, K] */
+    const uint16_t *bias;  /* [N] or null */
+    uint16_t *c;           /* [M, N] */
+    uint32_t m, n, k;      /* n = output columns */
+    uint32_t tiles_m, tiles_n;
+    uint32_t x_bytes, w_bytes;
+};
+
+template <int EPI>
+__global__ void __launch_bounds__(HK_GEMM_THREADS, 1)
+hk_gemm_mfma(hk_gemm_args g) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t hk_smem[];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63, wave = tid >> 6;
+    const uint32_t wm = wave & 1, wn = wave >> 1;
+
+    /* ---- workgroup -> tile (XCD regroup, then GROUP_M bands) ---- */
+    uint32_t pid = blockIdx.x;
+    const uint32_t nwg = gridDim.x;
+    if ((nwg & 7u) == 0) pid = (pid & 7u) * (nwg >> 3) + (pid >> 3);
+    const uint32_t band = HK_GROUP_M * g.tiles_n;
+    const uint32_t first_m = (pid / band) * HK_GROUP_M;
+    const uint32_t band_rows = min(g.tiles_m - first_m, (uint32_t)HK_GROUP_M);
+    const uint32_t in_band = pid % band;
+    const uint32_t tile_m = first_m + in_band % band_rows;
+    const uint32_t tile_n = in_band / band_rows;
+    const uint32_t m0 = tile_m * HK_BM;
+
+    /* ---- per-thread load plan: 8 chunks of X rows and of W rows ---- */
+    const __amdgpu_buffer_rsrc_t xr = hk_rsrc(g.x, g.x_bytes);
+    const __amdgpu_buffer_rsrc_t wr = hk_rsrc(g.w, g.w_bytes);
+    const uint32_t lc = tid & 7u;   /* chunk within the 64-k row slice */
+    const uint32_t lr = tid >> 3;   /* rows lr + 32 i */
+    uint32_t x_off[8], w_off[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint32_t row = lr + 32u * i;
+        /* rows past M: offset beyond the buffer -> zeros */
+        const uint32_t xm = m0 + row;
+        x_off[i] = xm < g.m ? (xm * g.k + lc * 8u) * 2u : 0xfffffff0u;
+        uint32_t wrow;
+        if (EPI == HK_EPI_SWIGLU) {
+            /* W tile rows: per wave half 64 gate rows then 64 up rows */
+            const uint32_t half = row >> 7, within = row & 127u;
+            const uint32_t col = tile_n * 128u + half * 64u + (within & 63u);
+            wrow = col < g.n ? (within >> 6) * g.n + col : 0xffffffffu;
+        } else {
+            wrow = tile_n * HK_BN + row;
+            if (wrow >= g.n) wrow = 0xffffffffu;
+        }
+        w_off[i] = wrow != 0xffffffffu ? (wrow * g.k + lc * 8u) * 2u
+                                       : 0xfffffff0u;
+    }
+
+    hk_f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    hk_v4i xs[8], ws[8];
+    auto load_global = [&](uint32_t k0) {
+        const uint32_t kb = k0 * 2u;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            xs[i] = __builtin_amdgcn_raw_buffer_load_b128(
+                xr, x_off[i] == 0xfffffff0u ? x_off[i] : x_off[i] + kb, 0, 0);
+            ws[i] = __builtin_amdgcn_raw_buffer_load_b128(
+                wr, w_off[i] == 0xfffffff0u ? w_off[i] : w_off[i] + kb, 0, 0);
+        }
+    };
+    auto store_lds = [&](uint32_t stage) {
+        uint8_t *sx = hk_smem + stage * (2 * HK_TILE_BYTES);
+        uint8_t *sw = sx + HK_TILE_BYTES;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t row = lr + 32u * i;
+            *(hk_v4i *)(sx + hk_swz(row, lc)) = xs[i];
+            *(hk_v4i *)(sw + hk_swz(row, lc)) = ws[i];
+        }
+    };
+
+    const uint32_t k_steps = g.k / HK_BK;
+    load_global(0);
+    store_lds(0);
+    __syncthreads();
+
+    const uint32_t frag_row = lane & 31u;
+    const uint32_t frag_half = lane >> 5;
+    for (uint32_t kt = 0; kt < k_steps; kt++) {
+        const uint32_t stage = kt & 1u;
+        if (kt + 1 < k_steps) load_global((kt + 1) * HK_BK);
+        const uint8_t *sx = hk_smem + stage * (2 * HK_TILE_BYTES);
+        const uint8_t *sw = sx + HK_TILE_BYTES;
+#pragma unroll
+        for (uint32_t ks = 0; ks < HK_BK / 16; ks++) {
+            const uint32_t chunk = ks * 2u + frag_half;
+            hk_bf16x8 wf[4], xf[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const uint32_t wrow = wn * 128u + t * 32u + frag_row;
+                const uint32_t xrow = wm * 128u + t * 32u + frag_row;
+                wf[t] = *(const hk_bf16x8 *)(sw + hk_swz(wrow, chunk));
+                xf[t] = *(const hk_bf16x8 *)(sx + hk_swz(xrow, chunk));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        wf[i], xf[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < k_steps) store_lds(stage ^ 1u);
+        __syncthreads();
+    }
+
+    /* ---- epilogue ----
+     * acc[i][j][r] = C[m][n] with
+     *   m = m0 + wm*128 + j*32 + lane%32
+     *   W-tile row = wn*128 + i*32 + (r/4)*8 + (lane/32)*4 + r%4 */
+    const uint32_t sub = frag_half * 4u;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t m = m0 + wm * 128u + j * 32u + frag_row;
+        if (m >= g.m) continue;
+        uint16_t *crow = g.c + (size_t)m * g.n;
+        if (EPI == HK_EPI_SWIGLU) {
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const uint32_t col = tile_n * 128u + wn * 64u + i * 32u +
+                                         q * 8u + sub;
+                    if (col >= g.n) continue;
+                    float out[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        float gate = hk_bf2f(hk_f2bf(acc[i][j][q * 4 + e]));
+                        float up = hk_bf2f(hk_f2bf(acc[i + 2][j][q * 4 + e]));
+                        out[e] = hk_silu_f(gate) * up;
+                    }
+                    uint2 packed = {hk_pack2(out[0], out[1]),
+                                    hk_pack2(out[2], out[3])};
+                    *(uint2 *)(crow + col) = packed;
+                }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const uint32_t col = tile_n * HK_BN + wn * 128u + i * 32u +
+                                         q * 8u + sub;
+                    if (col >= g.n) continue;
+                    float out[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) out[e] = acc[i][j][q * 4 + e];
+                    if (g.bias) {
+                        uint2 b = *(const uint2 *)(g.bias + col);
+                        out[0] += hk_bf2f(b.x & 0xffffu);
+                        out[1] += hk_bf2f(b.x >> 16);
+                        out[2] += hk_bf2f(b.y & 0xffffu);
+                        out[3] += hk_bf2f(b.y >> 16);
+                    }
+                    if (EPI == HK_EPI_GELU) {
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            out[e] = hk_gelu_tanh_f(hk_bf2f(hk_f2bf(out[e])));
+                    }
+                    uint2 packed = {hk_pack2(out[0], out[1]),
+                                    hk_pack2(out[2], out[3])};
+                    *(uint2 *)(crow + col) = packed;
+                }
+        }
+    }
+}
+
+/* Sequential-k reference GEMM (any shape).  For SwiGLU it writes the fused
+ * [M, 2N] bf16 projection into `c` (caller runs the activation). */
+__global__ void hk_gemm_reference(const uint16_t *x, const uint16_t *w,
+                                  const uint16_t *bias, uint16_t *c,
+                                  uint32_t m, uint32_t n, uint32_t k,
+                                  int gelu) {
+    uint32_t col = blockIdx.x * blockDim.x + threadIdx.x;
+    uint32_t row = blockIdx.y;
+    if (row >= m || col >= n) return;
+    float sum = bias ? hk_bf2f(bias[col]) : 0.0f;
+    const uint16_t *xr = x + (size_t)row * k;
+    const uint16_t *wr = w + (size_t)col * k;
+    for (uint32_t i = 0; i < k; i++)
+        sum = fmaf(hk_bf2f(xr[i]), hk_bf2f(wr[i]), sum);
+    if (gelu) sum = hk_gelu_tanh_f(hk_bf2f(hk_f2bf(sum)));
+    c[(size_t)row * n + col] = hk_f2bf(sum);
+}
+
+__global__ void hk_swiglu_rows(const uint16_t *fused, uint16_t *out,
+                               uint32_t rows, uint32_t width) {
+    size_t index = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (index >= (size_t)rows * width) return;
+    size_t row = index / width, col = index % width;
+    float gate = hk_bf2f(fused[row * 2 * width + col]);
+    float up = hk_bf2f(fused[row * 2 * width + width + col]);
+    out[index] = hk_f2bf(hk_silu_f(gate) * up);
+}
+
+static bool hk_gemm_lds_ready = false;
+
+int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
+                 const uint16_t *bias, uint16_t *c, uint32_t m, uint32_t n,
+                 uint32_t k, int epilogue) {
+    if (!m || !n) return 1;
+    const uint64_t w_rows = epilogue == HK_EPI_SWIGLU ? 2ull * n : n;
+    const uint64_t x_bytes = (uint64_t)m * k * 2, w_bytes = w_rows * k * 2;
+    const bool mfma = !gpu->reference_kernels && k % HK_BK == 0 && k > 0 &&
+                      n % 4 == 0 && x_bytes < 0xfffff000ull &&
+                      w_bytes < 0xfffff000ull &&
+                      (epilogue != HK_EPI_SWIGLU || n % 64 == 0) &&
+                      ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 &&
+                      ((uintptr_t)c & 7) == 0 && ((uintptr_t)bias & 7) == 0;
+    if (mfma) {
+        if (!hk_gemm_lds_ready) {
+            (void)hipFuncSetAttribute(
+                (const void *)hk_gemm_mfma<HK_EPI_STORE>,
+                hipFuncAttributeMaxDynamicSharedMemorySize, HK_GEMM_LDS);
+            (void)hipFuncSetAttribute(
+                (const void *)hk_gemm_mfma<HK_EPI_SWIGLU>,
+                hipFuncAttributeMaxDynamicSharedMemorySize, HK_GEMM_LDS);
+            (void)hipFuncSetAttribute(
+                (const void *)hk_gemm_mfma<HK_EPI_GELU>,
+                hipFuncAttributeMaxDynamicSharedMemorySize, HK_GEMM_LDS);
+            hk_gemm_lds_ready = true;
+        }
+        hk_gemm_args g;
+        g.x = x; g.w = w; g.bias = bias; g.c = c;
+        g.m = m; g.n = n; g.k = k;
+        g.tiles_m = (m + HK_BM - 1) / HK_BM;
+        const uint32_t cols_per_tile = epilogue == HK_EPI_SWIGLU ? 128 : HK_BN;
+        g.tiles_n = (n + cols_per_tile - 1) / cols_per_tile;
+        g.x_bytes = (uint32_t)x_bytes;
+        g.w_bytes = (uint32_t)w_bytes;
+        dim3 grid(g.tiles_m * g.tiles_n);
+        if (epilogue == HK_EPI_SWIGLU)
+            hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_SWIGLU>, grid,
+                               dim3(HK_GEMM_THREADS), HK_GEMM_LDS, gpu->stream,
+                               g);
+        else if (epilogue == HK_EPI_GELU)
+            hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_GELU>, grid,
+                               dim3(HK_GEMM_THREADS), HK_GEMM_LDS, gpu->stream,
+                               g);
+        else
+            hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_STORE>, grid,
+                               dim3(HK_GEMM_THREADS), HK_GEMM_LDS, gpu->stream,
+                               g);
+        return 1;
+    }
+    if (epilogue == HK_EPI_SWIGLU) {
+        uint16_t *fused = (uint16_t *)hk_workspace(gpu, (size_t)m * n * 4);
+        if (!fused) return 0;
+        hipLaunchKernelGGL(hk_gemm_reference, dim3((2 * n + 255) / 256, m),
+                           dim3(256), 0, gpu->stream, x, w, bias, fused, m,
+                           2 * n, k, 0);
+        size_t count = (size_t)m * n;
+        hipLaunchKernelGGL(hk_swiglu_rows, dim3((unsigned)((count + 255) / 256)),
+                           dim3(256), 0, gpu->stream, fused, c, m, n);
+        return 1;
+    }
+    hipLaunchKernelGGL(hk_gemm_reference, dim3((n + 255) / 256, m), dim3(256),
+                       0, gpu->stream, x, w, bias, c, m, n, k,
+                       epilogue == HK_EPI_GELU ? 1 : 0);
+    return 1;
+}
+
+/* ================================================================ ops */
+
+extern "C" {
+
+static int hk_linear_kind(uint32_t rows, uint32_t in, uint32_t out) {
+    return rows >= 32 && in >= 256 && out >= 256 ? HK_KIND_LINEAR
+                                                 : HK_KIND_DIRECT;
+}
+
+int h3_gpu_linear_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                       const h3_gpu_tensor *input, const h3_gpu_tensor *weight,
+                       const h3_gpu_tensor *bias, uint32_t rows,
+                       uint32_t input_dim, uint32_t output_dim) {
+    if (!hk_require(gpu, input, (size_t)rows * input_dim, H3_GPU_BF16,
+                    "linear input") ||
+        !hk_require(gpu, weight, (size_t)output_dim * input_dim, H3_GPU_BF16,
+                    "linear weight") ||
+        !hk_require(gpu, output, (size_t)rows * output_dim, H3_GPU_BF16,
+                    "linear output") ||
+        (bias && !hk_require(gpu, bias, output_dim, H3_GPU_BF16,
+                             "linear bias")) ||
+        !hk_require_active(gpu))
+        return 0;
+    hk_op_begin(gpu, "gemm");
+    if (!hk_gemm_bf16(gpu, HK_CBF16(input), HK_CBF16(weight),
+                      bias ? HK_CBF16(bias) : NULL, HK_BF16(output), rows,
+                      output_dim, input_dim, HK_EPI_STORE))
+        return 0;
+    return hk_op_end(gpu, "gemm", hk_linear_kind(rows, input_dim, output_dim));
+}
+
+int h3_gpu_linear_gelu_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                            const h3_gpu_tensor *input,
+                            const h3_gpu_tensor *weight,
+                            const h3_gpu_tensor *bias, uint32_t rows,
+                            uint32_t input_dim, uint32_t output_dim) {
+    if (!hk_require(gpu, input, (size_t)rows * input_dim, H3_GPU_BF16,
+                    "linear input") ||
+        !hk_require(gpu, weight, (size_t)output_dim * input_dim, H3_GPU_BF16,
+                    "linear weight") ||
+        !hk_require(gpu, output, (size_t)rows * output_dim, H3_GPU_BF16,
+                    "linear output") ||
+        (bias && !hk_require(gpu, bias, output_dim, H3_GPU_BF16,
+                             "linear bias")) ||
+        !hk_require_active(gpu))
+        return 0;
+    hk_op_begin(gpu, "gemm_gelu");
+    if (!hk_gemm_bf16(gpu, HK_CBF16(input), HK_CBF16(weight),
+                      bias ? HK_CBF16(bias) : NULL, HK_BF16(output), rows,
+                      output_dim, input_dim, HK_EPI_GELU))
+        return 0;
+    return hk_op_end(gpu, "gemm_gelu",
+                     hk_linear_kind(rows, input_dim, output_dim));
+}
+
+int h3_gpu_mlp_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                    const h3_gpu_tensor *input,
+                    const h3_gpu_tensor *fc1_weight,
+                    const h3_gpu_tensor *fc2_weight, uint32_t rows,
+                    uint32_t input_dim, uint32_t hidden_dim,
+                    uint32_t output_dim) {
+    if (!hk_require(gpu, input, (size_t)rows * input_dim, H3_GPU_BF16,
+                    "MLP input") ||
+        !hk_require(gpu, fc1_weight, (size_t)hidden_dim * 2 * input_dim,
+                    H3_GPU_BF16, "MLP fc1 weight") ||
+        !hk_require(gpu, fc2_weight, (size_t)output_dim * hidden_dim,
+                    H3_GPU_BF16, "MLP fc2 weight") ||
+        !hk_require(gpu, output, (size_t)rows * output_dim, H3_GPU_BF16,
+                    "MLP output") ||
+        !hk_require_active(gpu))
+        return 0;
+    size_t activated_bytes = (size_t)rows * hidden_dim * 2;
+    /* the reference-kernel SwiGLU path also needs 2x that for the fused
+     * projection; keep the activation after it */
+    size_t fused_bytes = gpu->reference_kernels ? activated_bytes * 2 : 0;
+    fused_bytes = (fused_bytes + 255) & ~(size_t)255;
+    uint8_t *base = (uint8_t *)hk_workspace(gpu, fused_bytes + activated_bytes);
+    if (!base) return 0;
+    uint16_t *activated = (uint16_t *)(base + fused_bytes);
+    hk_op_begin(gpu, "gemm_swiglu");
+    if (!hk_gemm_bf16(gpu, HK_CBF16(input), HK_CBF16(fc1_weight), NULL,
+                      activated, rows, hidden_dim, input_dim, HK_EPI_SWIGLU))
+        return 0;
+    if (!hk_op_end(gpu, "gemm_swiglu", HK_KIND_LINEAR)) return 0;
+    hk_op_begin(gpu, "gemm");
+    if (!hk_gemm_bf16(gpu, activated, HK_CBF16(fc2_weight), NULL,
+                      HK_BF16(output), rows, output_dim, hidden_dim,
+                      HK_EPI_STORE))
+        return 0;
+    return hk_op_end(gpu, "gemm", HK_KIND_LINEAR);
+}
+
+int h3_gpu_ffn_gelu_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                         h3_gpu_tensor *activated,
+                         const h3_gpu_tensor *input,
+                         const h3_gpu_tensor *fc1_weight,
+                         const h3_gpu_tensor *fc1_bias,
+                         const h3_gpu_tensor *fc2_weight,
+                         const h3_gpu_tensor *fc2_bias, uint32_t rows,
+                         uint32_t input_dim, uint32_t hidden_dim,
+                         uint32_t output_dim) {
+    if (!hk_require(gpu, input, (size_t)rows * input_dim, H3_GPU_BF16,
+                    "FFN input") ||
+        !hk_require(gpu, fc1_weight, (size_t)hidden_dim * input_dim,
+                    H3_GPU_BF16, "FFN fc1 weight") ||
+        !hk_require(gpu, fc2_weight, (size_t)output_dim * hidden_dim,
+                    H3_GPU_BF16, "FFN fc2 weight") ||
+        (fc1_bias && !hk_require(gpu, fc1_bias, hidden_dim, H3_GPU_BF16,
+                                 "FFN fc1 bias")) ||
+        (fc2_bias && !hk_require(gpu, fc2_bias, output_dim, H3_GPU_BF16,
+                                 "FFN fc2 bias")) ||
+        (activated && !hk_require(gpu, activated, (size_t)rows * hidden_dim,
+                                  H3_GPU_BF16, "FFN activation")) ||
+        !hk_require(gpu, output, (size_t)rows * output_dim, H3_GPU_BF16,
+                    "FFN output") ||
+        !hk_require_active(gpu))
+        return 0;
+    uint16_t *act = activated ? HK_BF16(activated)
+                              : (uint16_t *)hk_workspace(
+                                    gpu, (size_t)rows * hidden_dim * 2);
+    if (!act) return 0;
+    hk_op_begin(gpu, "gemm_gelu");
+    if (!hk_gemm_bf16(gpu, HK_CBF16(input), HK_CBF16(fc1_weight),
+                      fc1_bias ? HK_CBF16(fc1_bias) : NULL, act, rows,
+                      hidden_dim, input_dim, HK_EPI_GELU))
+        return 0;
+    if (!hk_op_end(gpu, "gemm_gelu", HK_KIND_LINEAR)) return 0;
+    hk_op_begin(gpu, "gemm");
+    if (!hk_gemm_bf16(gpu, act, HK_CBF16(fc2_weight),
+                      fc2_bias ? HK_CBF16(fc2_bias) : NULL, HK_BF16(output),
+                      rows, output_dim, hidden_dim, HK_EPI_STORE))
+        return 0;
+    return hk_op_end(gpu, "gemm", HK_KIND_LINEAR);
+}
+
+int h3_gpu_grouped_qkv_linear_rope_bf16(
+    h3_gpu *gpu, h3_gpu_tensor *query, h3_gpu_tensor *key,
+    h3_gpu_tensor *value, h3_gpu_tensor *qkv, const h3_gpu_tensor *input,
+    const h3_gpu_tensor *weight, const h3_gpu_tensor *q_norm,
+    const h3_gpu_tensor *k_norm, const h3_gpu_tensor *rope_cos,
+    const h3_gpu_tensor *rope_sin, uint32_t rows, uint32_t input_dim,
+    uint32_t heads, uint32_t head_dim, uint32_t rope_half, float epsilon) {
+    uint32_t out_dim = heads * head_dim * 3;
+    return h3_gpu_linear_bf16(gpu, qkv, input, weight, NULL, rows, input_dim,
+                              out_dim) &&
+           h3_gpu_grouped_qkv_rope_bf16(gpu, query, key, value, qkv, q_norm,
+                                        k_norm, rope_cos, rope_sin, rows,
+                                        heads, head_dim, rope_half, epsilon);
+}
+
+} /* extern "C" */

@@ -1,0 +1,137 @@
+/* Internal definitions of the MI355X HIP backend of h3_gpu.h.
+ *
+ * Execution model: one context owns one HIP stream (default priority) on
+ * device 0.  Every op enqueues its kernels on that stream, so the stream's
+ * order is the program order; h3_gpu_submit() waits for the stream.  This
+ * is the same ordering contract as the reference's single in-order queue
+ * (reference h3_cuda_internal.h:1-5, h3_gpu_cuda.cu:890-905).
+ */
+#ifndef HK_INTERNAL_H
+#define HK_INTERNAL_H
+
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/h3_gpu.h"
+#include "../../include/h3_hip.h"
+
+struct h3_gpu_tensor {
+    void *data;
+    size_t elements;
+    size_t bytes;
+    h3_gpu_dtype dtype;
+    struct h3_gpu *owner;
+};
+
+struct hk_cache_block;
+struct hk_timing;
+
+struct h3_gpu {
+    int device;
+    hipStream_t stream;
+    int active;
+    char error[512];
+    h3_gpu_stats stats;
+    double batch_start;
+    char profile_label[128];
+    h3_gpu_stats profile_mark_stats;
+    double profile_mark_wall;
+    /* exact-size cache of freed device blocks */
+    struct hk_cache_block *cache;
+    size_t cache_bytes;
+    size_t cache_limit;
+    /* grow-only device scratch for op intermediates */
+    void *workspace;
+    size_t workspace_bytes;
+    /* H3_HIP_REFERENCE=1: route GEMM and attention through the simple
+     * (sequential-k / two-pass) reference kernels */
+    int reference_kernels;
+    /* per-op event timing */
+    struct hk_timing *timing;
+    hipEvent_t markers[16];
+    int marker_valid[16];
+    int num_cus;
+};
+
+/* stats kinds, mirroring the reference counters (h3_cuda_internal.h:142-160) */
+enum { HK_KIND_DIRECT = 0, HK_KIND_LINEAR = 1, HK_KIND_CONV = 2,
+       HK_KIND_SDPA = 3 };
+
+static inline size_t hk_item_size(h3_gpu_dtype dtype) {
+    return dtype == H3_GPU_BF16 ? 2 : dtype == H3_GPU_I8 ? 1 : 4;
+}
+
+static inline int hk_fail(struct h3_gpu *gpu, const char *format, ...) {
+    if (gpu) {
+        va_list arguments;
+        va_start(arguments, format);
+        vsnprintf(gpu->error, sizeof(gpu->error), format, arguments);
+        va_end(arguments);
+    }
+    return 0;
+}
+
+static inline int hk_fail_hip(struct h3_gpu *gpu, const char *what,
+                              hipError_t status) {
+    return hk_fail(gpu, "HIP %s failed: %s", what, hipGetErrorString(status));
+}
+
+static inline int hk_require_active(struct h3_gpu *gpu) {
+    if (!gpu || !gpu->active) return hk_fail(gpu, "no active command buffer");
+    return 1;
+}
+
+static inline int hk_require(struct h3_gpu *gpu, const h3_gpu_tensor *tensor,
+                             size_t elements, h3_gpu_dtype dtype,
+                             const char *label) {
+    if (!tensor || tensor->elements < elements)
+        return hk_fail(gpu, "%s tensor is too small", label);
+    if (tensor->dtype != dtype)
+        return hk_fail(gpu, "%s tensor has the wrong dtype", label);
+    return 1;
+}
+
+#define HK_BF16(t) ((uint16_t *)(t)->data)
+#define HK_CBF16(t) ((const uint16_t *)(t)->data)
+#define HK_F32(t) ((float *)(t)->data)
+#define HK_CF32(t) ((const float *)(t)->data)
+#define HK_CU32(t) ((const uint32_t *)(t)->data)
+
+/* Op bracket: hk_op_begin() records a start event when timing is on;
+ * hk_op_end() checks the launch, records the stop event and bumps the
+ * stats counter of the given kind.  Returns 1/0 like the public ops. */
+void hk_op_begin(struct h3_gpu *gpu, const char *name);
+int hk_op_end(struct h3_gpu *gpu, const char *name, int kind);
+
+/* Grow-only device scratch shared by ops of one context. */
+void *hk_workspace(struct h3_gpu *gpu, size_t bytes);
+
+double hk_now(void);
+
+/* ---------------------------------------------------------------- launch
+ * helpers implemented in the kernel translation units.  All take device
+ * pointers and enqueue on gpu->stream; shapes are validated by the caller.
+ */
+
+/* GEMM epilogues */
+enum { HK_EPI_STORE = 0, HK_EPI_SWIGLU = 1, HK_EPI_GELU = 2 };
+
+/* C[M,N] = epi(A[M,K] . W[N,K]^T + bias).  For HK_EPI_SWIGLU the weight has
+ * 2*N rows (gate rows [0,N), up rows [N,2N)) and C is the [M,N] activation.
+ * ldc is the row stride of C in elements. */
+int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *a, const uint16_t *w,
+                 const uint16_t *bias, uint16_t *c, uint32_t m, uint32_t n,
+                 uint32_t k, int epilogue);
+
+/* Flash attention; q rows [q_rows][heads][hd], k/v [kv_rows][heads][hd].
+ * head_major selects [heads][q_rows][hd] output. */
+int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
+                      const uint16_t *k, const uint16_t *v, uint16_t *o,
+                      uint32_t q_rows, uint32_t kv_rows, uint32_t heads,
+                      uint32_t head_dim, float scale, int head_major);
+
+#endif

@@ -1,0 +1,482 @@
+/* DiT denoiser driver over the h3_gpu.h device API; see h3hip_dit.h. */
+#include "h3hip_dit.h"
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+enum { SLOTS = 6 };
+
+typedef struct {
+    h3_gpu_tensor *norm1, *norm2, *norm3, *norm3_bias;
+    h3_gpu_tensor *qkv, *qkv_bias, *q_norm, *k_norm, *out, *out_bias;
+    h3_gpu_tensor *fc1, *fc1_bias, *fc2, *fc2_bias;
+    h3_gpu_tensor *cq, *cq_bias, *ck, *ck_bias, *cv, *cv_bias;
+    h3_gpu_tensor *cq_norm, *ck_norm, *co, *co_bias;
+    h3_gpu_tensor *modulation;
+} h3hip_block;
+
+struct h3hip_dit {
+    h3_gpu *gpu;
+    h3hip_dit_config config;
+    uint32_t modalities; /* H3: 3 tags per time row; Wan: 1 */
+    h3hip_block *blocks;
+    /* shared state and activations */
+    h3_gpu_tensor *hidden, *row_map, *rope_cos, *rope_sin, *context;
+    h3_gpu_tensor *mod_a, *mod_b, *qkv, *query, *key, *value, *attn, *proj;
+    h3_gpu_tensor *cross_q, *cross_k, *cross_v, *cross_out;
+    int attention_adaln_ready;
+    char error[512];
+};
+
+static int dit_fail(h3hip_dit *dit, const char *format, ...) {
+    va_list arguments;
+    va_start(arguments, format);
+    vsnprintf(dit->error, sizeof(dit->error), format, arguments);
+    va_end(arguments);
+    return 0;
+}
+
+static int dit_op(h3hip_dit *dit, int ok, const char *what) {
+    if (ok) return 1;
+    return dit_fail(dit, "%s: %s", what, h3_gpu_error(dit->gpu));
+}
+
+const char *h3hip_dit_error(const h3hip_dit *dit) {
+    return dit ? dit->error : "no DiT";
+}
+
+static int is_wan(const h3hip_dit *dit) {
+    return dit->config.family == H3HIP_FAMILY_WAN;
+}
+
+/* ------------------------------------------------------------ FLOPs */
+
+double h3hip_dit_block_gemm_flops(const h3hip_dit_config *c) {
+    double d = c->hidden, inner = (double)c->heads * c->head_dim;
+    double n = c->rows, f = c->ffn;
+    if (c->family == H3HIP_FAMILY_WAN) {
+        double t = c->text_rows;
+        /* qkv, out, cross q, cross out, ffn up + down; cross k,v on text */
+        return 2.0 * n * (3 * d * inner + inner * d + d * inner + inner * d +
+                          2 * d * f) +
+               2.0 * t * (2 * d * inner);
+    }
+    /* qkv (3 inner), out, fc1 (2 ffn), fc2 */
+    return 2.0 * n * (3 * d * inner + inner * d + 2 * d * f + f * d);
+}
+
+double h3hip_dit_block_attention_flops(const h3hip_dit_config *c) {
+    double inner = (double)c->heads * c->head_dim, n = c->rows;
+    double flops = 4.0 * n * n * inner;
+    if (c->family == H3HIP_FAMILY_WAN) flops += 4.0 * n * c->text_rows * inner;
+    return flops;
+}
+
+double h3hip_dit_block_flops(const h3hip_dit_config *c) {
+    return h3hip_dit_block_gemm_flops(c) + h3hip_dit_block_attention_flops(c);
+}
+
+/* --------------------------------------------------------- lifetime */
+
+static h3_gpu_tensor *bf16(h3hip_dit *dit, size_t n, int *ok) {
+    h3_gpu_tensor *t = h3_gpu_tensor_new_bf16(dit->gpu, n);
+    if (!t) *ok = 0;
+    return t;
+}
+
+h3hip_dit *h3hip_dit_create(h3_gpu *gpu, const h3hip_dit_config *config,
+                            char *error, size_t error_size) {
+    if (!gpu || !config || !config->hidden || !config->heads ||
+        !config->head_dim || !config->ffn || !config->blocks ||
+        !config->rows || !config->time_rows ||
+        config->rope_half * 2 > config->head_dim ||
+        (config->family == H3HIP_FAMILY_WAN && !config->text_rows)) {
+        if (error && error_size)
+            snprintf(error, error_size, "invalid DiT configuration");
+        return NULL;
+    }
+    h3hip_dit *dit = (h3hip_dit *)calloc(1, sizeof(*dit));
+    if (!dit) return NULL;
+    dit->gpu = gpu;
+    dit->config = *config;
+    dit->modalities = config->family == H3HIP_FAMILY_WAN ? 1u : 3u;
+    dit->blocks = (h3hip_block *)calloc(config->blocks, sizeof(h3hip_block));
+    if (!dit->blocks) {
+        free(dit);
+        return NULL;
+    }
+    const size_t d = config->hidden;
+    const size_t inner = (size_t)config->heads * config->head_dim;
+    const size_t n = config->rows, f = config->ffn, hd = config->head_dim;
+    const size_t t = config->text_rows;
+    int ok = 1;
+    for (uint32_t b = 0; b < config->blocks && ok; b++) {
+        h3hip_block *w = &dit->blocks[b];
+        w->norm1 = bf16(dit, d, &ok);
+        w->norm2 = bf16(dit, d, &ok);
+        w->q_norm = bf16(dit, hd, &ok);
+        w->k_norm = bf16(dit, hd, &ok);
+        w->qkv = bf16(dit, 3 * inner * d, &ok);
+        w->out = bf16(dit, d * inner, &ok);
+        w->modulation = bf16(dit, (size_t)config->time_rows *
+                                      dit->modalities * SLOTS * d, &ok);
+        if (is_wan(dit)) {
+            w->qkv_bias = bf16(dit, 3 * inner, &ok);
+            w->out_bias = bf16(dit, d, &ok);
+            w->norm3 = bf16(dit, d, &ok);
+            w->norm3_bias = bf16(dit, d, &ok);
+            w->cq = bf16(dit, inner * d, &ok);
+            w->cq_bias = bf16(dit, inner, &ok);
+            w->ck = bf16(dit, inner * d, &ok);
+            w->ck_bias = bf16(dit, inner, &ok);
+            w->cv = bf16(dit, inner * d, &ok);
+            w->cv_bias = bf16(dit, inner, &ok);
+            w->cq_norm = bf16(dit, hd, &ok);
+            w->ck_norm = bf16(dit, hd, &ok);
+            w->co = bf16(dit, d * inner, &ok);
+            w->co_bias = bf16(dit, d, &ok);
+            w->fc1 = bf16(dit, f * d, &ok);
+            w->fc1_bias = bf16(dit, f, &ok);
+            w->fc2 = bf16(dit, d * f, &ok);
+            w->fc2_bias = bf16(dit, d, &ok);
+        } else {
+            w->fc1 = bf16(dit, 2 * f * d, &ok);
+            w->fc2 = bf16(dit, d * f, &ok);
+        }
+    }
+    dit->hidden = bf16(dit, n * d, &ok);
+    dit->row_map = ok ? h3_gpu_tensor_from_u32(gpu, NULL, n) : NULL;
+    if (!dit->row_map) ok = 0;
+    dit->rope_cos = bf16(dit, n * config->rope_half + 1, &ok);
+    dit->rope_sin = bf16(dit, n * config->rope_half + 1, &ok);
+    dit->mod_a = bf16(dit, n * d, &ok);
+    dit->mod_b = bf16(dit, n * d, &ok);
+    dit->qkv = bf16(dit, n * 3 * inner, &ok);
+    dit->query = bf16(dit, n * inner, &ok);
+    dit->key = bf16(dit, n * inner, &ok);
+    dit->value = bf16(dit, n * inner, &ok);
+    dit->attn = bf16(dit, n * inner, &ok);
+    dit->proj = bf16(dit, n * d, &ok);
+    if (is_wan(dit)) {
+        dit->context = bf16(dit, t * d, &ok);
+        dit->cross_q = bf16(dit, n * inner, &ok);
+        dit->cross_k = bf16(dit, t * inner, &ok);
+        dit->cross_v = bf16(dit, t * inner, &ok);
+        dit->cross_out = bf16(dit, n * inner, &ok);
+    }
+    if (!ok) {
+        if (error && error_size)
+            snprintf(error, error_size, "cannot allocate DiT tensors: %s",
+                     h3_gpu_error(gpu));
+        h3hip_dit_free(dit);
+        return NULL;
+    }
+    return dit;
+}
+
+void h3hip_dit_free(h3hip_dit *dit) {
+    if (!dit) return;
+    if (dit->blocks) {
+        for (uint32_t b = 0; b < dit->config.blocks; b++) {
+            h3_gpu_tensor **fields = (h3_gpu_tensor **)&dit->blocks[b];
+            size_t count = sizeof(h3hip_block) / sizeof(h3_gpu_tensor *);
+            for (size_t i = 0; i < count; i++) h3_gpu_tensor_free(fields[i]);
+        }
+        free(dit->blocks);
+    }
+    h3_gpu_tensor *shared[] = {
+        dit->hidden, dit->row_map, dit->rope_cos, dit->rope_sin,
+        dit->context, dit->mod_a, dit->mod_b, dit->qkv, dit->query,
+        dit->key, dit->value, dit->attn, dit->proj, dit->cross_q,
+        dit->cross_k, dit->cross_v, dit->cross_out};
+    for (size_t i = 0; i < sizeof(shared) / sizeof(*shared); i++)
+        h3_gpu_tensor_free(shared[i]);
+    free(dit);
+}
+
+h3_gpu_tensor *h3hip_dit_tensor(h3hip_dit *dit, const char *name,
+                                uint32_t block) {
+    if (!dit || !name) return NULL;
+    if (!strcmp(name, "hidden")) return dit->hidden;
+    if (!strcmp(name, "row_map")) return dit->row_map;
+    if (!strcmp(name, "rope_cos")) return dit->rope_cos;
+    if (!strcmp(name, "rope_sin")) return dit->rope_sin;
+    if (!strcmp(name, "context")) return dit->context;
+    if (block >= dit->config.blocks) return NULL;
+    h3hip_block *w = &dit->blocks[block];
+    struct { const char *name; h3_gpu_tensor *tensor; } table[] = {
+        {"norm1", w->norm1}, {"norm2", w->norm2}, {"norm3", w->norm3},
+        {"norm3_bias", w->norm3_bias}, {"qkv", w->qkv},
+        {"qkv_bias", w->qkv_bias}, {"q_norm", w->q_norm},
+        {"k_norm", w->k_norm}, {"out", w->out}, {"out_bias", w->out_bias},
+        {"fc1", w->fc1}, {"fc1_bias", w->fc1_bias}, {"fc2", w->fc2},
+        {"fc2_bias", w->fc2_bias}, {"cq", w->cq}, {"cq_bias", w->cq_bias},
+        {"ck", w->ck}, {"ck_bias", w->ck_bias}, {"cv", w->cv},
+        {"cv_bias", w->cv_bias}, {"cq_norm", w->cq_norm},
+        {"ck_norm", w->ck_norm}, {"co", w->co}, {"co_bias", w->co_bias},
+        {"modulation", w->modulation}};
+    for (size_t i = 0; i < sizeof(table) / sizeof(*table); i++)
+        if (!strcmp(name, table[i].name)) return table[i].tensor;
+    return NULL;
+}
+
+/* ------------------------------------------------------------- init */
+
+static int fill(h3hip_dit *dit, h3_gpu_tensor *t, uint64_t *seed, float mean,
+                float std) {
+    if (!t) return 1;
+    return h3_gpu_fill_normal_bf16(dit->gpu, t, 0, h3_gpu_tensor_elements(t),
+                                   (*seed)++, mean, std);
+}
+
+int h3hip_dit_init_random(h3hip_dit *dit, uint64_t seed, float weight_std,
+                          float mod_std) {
+    if (!dit) return 0;
+    h3_gpu *gpu = dit->gpu;
+    if (!dit_op(dit, h3_gpu_begin(gpu), "begin DiT init")) return 0;
+    uint64_t s = seed * 1000003ull + 17;
+    int ok = 1;
+    for (uint32_t b = 0; b < dit->config.blocks && ok; b++) {
+        h3hip_block *w = &dit->blocks[b];
+        ok = fill(dit, w->norm1, &s, 1.0f, 0.02f) &&
+             fill(dit, w->norm2, &s, 1.0f, 0.02f) &&
+             fill(dit, w->norm3, &s, 1.0f, 0.02f) &&
+             fill(dit, w->norm3_bias, &s, 0.0f, 0.02f) &&
+             fill(dit, w->q_norm, &s, 1.0f, 0.02f) &&
+             fill(dit, w->k_norm, &s, 1.0f, 0.02f) &&
+             fill(dit, w->cq_norm, &s, 1.0f, 0.02f) &&
+             fill(dit, w->ck_norm, &s, 1.0f, 0.02f) &&
+             fill(dit, w->qkv, &s, 0.0f, weight_std) &&
+             fill(dit, w->qkv_bias, &s, 0.0f, 0.02f) &&
+             fill(dit, w->out, &s, 0.0f, weight_std) &&
+             fill(dit, w->out_bias, &s, 0.0f, 0.02f) &&
+             fill(dit, w->cq, &s, 0.0f, weight_std) &&
+             fill(dit, w->cq_bias, &s, 0.0f, 0.02f) &&
+             fill(dit, w->ck, &s, 0.0f, weight_std) &&
+             fill(dit, w->ck_bias, &s, 0.0f, 0.02f) &&
+             fill(dit, w->cv, &s, 0.0f, weight_std) &&
+             fill(dit, w->cv_bias, &s, 0.0f, 0.02f) &&
+             fill(dit, w->co, &s, 0.0f, weight_std) &&
+             fill(dit, w->co_bias, &s, 0.0f, 0.02f) &&
+             fill(dit, w->fc1, &s, 0.0f, weight_std) &&
+             fill(dit, w->fc1_bias, &s, 0.0f, 0.02f) &&
+             fill(dit, w->fc2, &s, 0.0f, weight_std) &&
+             fill(dit, w->fc2_bias, &s, 0.0f, 0.02f) &&
+             fill(dit, w->modulation, &s, 0.0f, mod_std);
+    }
+    ok = ok && fill(dit, dit->hidden, &s, 0.0f, 1.0f) &&
+         fill(dit, dit->context, &s, 0.0f, 1.0f);
+    if (!ok) {
+        dit_fail(dit, "random init: %s", h3_gpu_error(gpu));
+        (void)h3_gpu_submit(gpu);
+        return 0;
+    }
+    if (!dit_op(dit, h3_gpu_submit(gpu), "submit DiT init")) return 0;
+    /* default row map: every row on time row 0 with tag 0; default RoPE:
+     * identity (cos 1, sin 0) */
+    size_t n = dit->config.rows, half = dit->config.rope_half;
+    uint32_t *map = (uint32_t *)calloc(n, sizeof(uint32_t));
+    float *c = (float *)malloc((n * half + 1) * sizeof(float));
+    float *z = (float *)calloc(n * half + 1, sizeof(float));
+    if (!map || !c || !z) {
+        free(map); free(c); free(z);
+        return dit_fail(dit, "out of memory");
+    }
+    for (size_t i = 0; i < n * half; i++) c[i] = 1.0f;
+    ok = h3hip_dit_set_row_map(dit, map) && h3hip_dit_set_rope(dit, c, z);
+    free(map); free(c); free(z);
+    return ok;
+}
+
+int h3hip_dit_set_row_map(h3hip_dit *dit, const uint32_t *row_map) {
+    if (!dit || !row_map) return 0;
+    uint32_t limit = dit->config.time_rows * dit->modalities;
+    for (uint32_t r = 0; r < dit->config.rows; r++)
+        if (row_map[r] >= limit)
+            return dit_fail(dit, "row map entry %u = %u exceeds %u modulation "
+                                 "rows", r, row_map[r], limit);
+    /* the kernels index mod[row_map[r]] directly: range checked above */
+    h3_gpu_tensor *fresh =
+        h3_gpu_tensor_from_u32(dit->gpu, row_map, dit->config.rows);
+    if (!fresh)
+        return dit_fail(dit, "row map upload: %s", h3_gpu_error(dit->gpu));
+    h3_gpu_tensor_free(dit->row_map);
+    dit->row_map = fresh;
+    return 1;
+}
+
+int h3hip_dit_set_rope(h3hip_dit *dit, const float *cosines,
+                       const float *sines) {
+    if (!dit || !cosines || !sines) return 0;
+    size_t count = (size_t)dit->config.rows * dit->config.rope_half;
+    if (!count) return 1;
+    h3_gpu *gpu = dit->gpu;
+    h3_gpu_tensor *c32 = h3_gpu_tensor_from_f32(gpu, cosines, count);
+    h3_gpu_tensor *s32 = h3_gpu_tensor_from_f32(gpu, sines, count);
+    int ok = c32 && s32 && h3_gpu_begin(gpu) &&
+             h3_gpu_cast_f32_to_bf16(gpu, dit->rope_cos, c32,
+                                     (uint32_t)count) &&
+             h3_gpu_cast_f32_to_bf16(gpu, dit->rope_sin, s32,
+                                     (uint32_t)count) &&
+             h3_gpu_submit(gpu);
+    h3_gpu_tensor_free(c32);
+    h3_gpu_tensor_free(s32);
+    return ok ? 1 : dit_fail(dit, "RoPE upload: %s", h3_gpu_error(gpu));
+}
+
+/* ------------------------------------------------------------ blocks */
+
+/* One H3 block, in the reference's order (h3_dit.c:2008-2180, BF16 path
+ * with fused gate+adaLN and the fused cross-block adaLN). */
+static int run_h3_block(h3hip_dit *dit, uint32_t index, int fuse_next) {
+    const h3hip_dit_config *c = &dit->config;
+    h3_gpu *gpu = dit->gpu;
+    h3hip_block *w = &dit->blocks[index];
+    const uint32_t rows = c->rows, hidden = c->hidden;
+    const uint32_t inner = c->heads * c->head_dim;
+    const float eps = c->epsilon;
+    const uint32_t slots = SLOTS;
+    if (!dit->attention_adaln_ready &&
+        !dit_op(dit, h3_gpu_adaln_bf16(gpu, dit->mod_a, dit->hidden,
+                                       w->norm1, w->modulation, dit->row_map,
+                                       rows, hidden, slots, 0, 1, eps),
+                "attention adaLN"))
+        return 0;
+    dit->attention_adaln_ready = 0;
+    if (!dit_op(dit, h3_gpu_grouped_qkv_linear_rope_bf16(
+                         gpu, dit->query, dit->key, dit->value, dit->qkv,
+                         dit->mod_a, w->qkv, w->q_norm, w->k_norm,
+                         dit->rope_cos, dit->rope_sin, rows, hidden, c->heads,
+                         c->head_dim, c->rope_half, eps),
+                "QKV projection/norm/RoPE") ||
+        !dit_op(dit, h3_gpu_sdpa_bf16(gpu, dit->attn, dit->query, dit->key,
+                                      dit->value, rows, c->heads, c->head_dim,
+                                      1.0f / sqrtf((float)c->head_dim)),
+                "joint attention") ||
+        !dit_op(dit, h3_gpu_linear_bf16(gpu, dit->proj, dit->attn, w->out,
+                                        NULL, rows, inner, hidden),
+                "attention output") ||
+        !dit_op(dit, h3_gpu_gate_adaln_bf16(
+                         gpu, dit->hidden, dit->mod_b, dit->hidden, dit->proj,
+                         w->norm2, w->modulation, w->modulation, dit->row_map,
+                         rows, hidden, slots, 2, 3, 4, eps),
+                "attention gate + MLP adaLN") ||
+        !dit_op(dit, h3_gpu_mlp_bf16(gpu, dit->proj, dit->mod_b, w->fc1,
+                                     w->fc2, rows, hidden, c->ffn, hidden),
+                "SwiGLU MLP"))
+        return 0;
+    if (fuse_next) {
+        h3hip_block *next = &dit->blocks[index + 1];
+        if (!dit_op(dit, h3_gpu_gate_adaln_bf16(
+                             gpu, dit->hidden, dit->mod_a, dit->hidden,
+                             dit->proj, next->norm1, w->modulation,
+                             next->modulation, dit->row_map, rows, hidden,
+                             slots, 5, 0, 1, eps),
+                    "MLP gate + next attention adaLN"))
+            return 0;
+        dit->attention_adaln_ready = 1;
+        return 1;
+    }
+    return dit_op(dit, h3_gpu_gate_bf16(gpu, dit->hidden, dit->hidden,
+                                        dit->proj, w->modulation, dit->row_map,
+                                        rows, hidden, slots, 5),
+                  "MLP gate");
+}
+
+/* One Wan-style block: self-attention, cross-attention, GELU FFN. */
+static int run_wan_block(h3hip_dit *dit, uint32_t index) {
+    const h3hip_dit_config *c = &dit->config;
+    h3_gpu *gpu = dit->gpu;
+    h3hip_block *w = &dit->blocks[index];
+    const uint32_t rows = c->rows, d = c->hidden, t = c->text_rows;
+    const uint32_t inner = c->heads * c->head_dim;
+    const float eps = c->epsilon;
+    const float scale = 1.0f / sqrtf((float)c->head_dim);
+    return dit_op(dit, h3_gpu_layer_adaln_bf16(
+                           gpu, dit->mod_a, dit->hidden, NULL, NULL,
+                           w->modulation, dit->row_map, rows, d, SLOTS, 0, 1,
+                           eps),
+                  "self-attention adaLN") &&
+           dit_op(dit, h3_gpu_linear_bf16(gpu, dit->qkv, dit->mod_a, w->qkv,
+                                          w->qkv_bias, rows, d, 3 * inner),
+                  "QKV projection") &&
+           dit_op(dit, h3_gpu_qkv_rope_bf16(
+                           gpu, dit->query, dit->key, dit->value, dit->qkv,
+                           w->q_norm, w->k_norm, dit->rope_cos, dit->rope_sin,
+                           rows, c->heads, c->head_dim, c->rope_half, eps),
+                  "Q/K norm + RoPE") &&
+           dit_op(dit, h3_gpu_sdpa_bf16(gpu, dit->attn, dit->query, dit->key,
+                                        dit->value, rows, c->heads,
+                                        c->head_dim, scale),
+                  "self-attention") &&
+           dit_op(dit, h3_gpu_linear_bf16(gpu, dit->proj, dit->attn, w->out,
+                                          w->out_bias, rows, inner, d),
+                  "self-attention output") &&
+           dit_op(dit, h3_gpu_gate_bf16(gpu, dit->hidden, dit->hidden,
+                                        dit->proj, w->modulation,
+                                        dit->row_map, rows, d, SLOTS, 2),
+                  "self-attention gate") &&
+           dit_op(dit, h3_gpu_layer_adaln_bf16(
+                           gpu, dit->mod_b, dit->hidden, w->norm3,
+                           w->norm3_bias, NULL, NULL, rows, d, SLOTS, 0, 0,
+                           eps),
+                  "cross-attention norm") &&
+           dit_op(dit, h3_gpu_linear_bf16(gpu, dit->cross_q, dit->mod_b,
+                                          w->cq, w->cq_bias, rows, d, inner),
+                  "cross Q projection") &&
+           dit_op(dit, h3_gpu_head_rms_norm_bf16(gpu, dit->cross_q,
+                                                 w->cq_norm, rows, c->heads,
+                                                 c->head_dim, eps),
+                  "cross Q norm") &&
+           dit_op(dit, h3_gpu_linear_bf16(gpu, dit->cross_k, dit->context,
+                                          w->ck, w->ck_bias, t, d, inner),
+                  "cross K projection") &&
+           dit_op(dit, h3_gpu_head_rms_norm_bf16(gpu, dit->cross_k,
+                                                 w->ck_norm, t, c->heads,
+                                                 c->head_dim, eps),
+                  "cross K norm") &&
+           dit_op(dit, h3_gpu_linear_bf16(gpu, dit->cross_v, dit->context,
+                                          w->cv, w->cv_bias, t, d, inner),
+                  "cross V projection") &&
+           dit_op(dit, h3_gpu_sdpa_cross_bf16(gpu, dit->cross_out,
+                                              dit->cross_q, dit->cross_k,
+                                              dit->cross_v, rows, t, c->heads,
+                                              c->head_dim, scale),
+                  "cross-attention") &&
+           dit_op(dit, h3_gpu_linear_bf16(gpu, dit->proj, dit->cross_out,
+                                          w->co, w->co_bias, rows, inner, d),
+                  "cross-attention output") &&
+           dit_op(dit, h3_gpu_add_bf16(gpu, dit->hidden, dit->hidden,
+                                       dit->proj, rows * d),
+                  "cross-attention residual") &&
+           dit_op(dit, h3_gpu_layer_adaln_bf16(
+                           gpu, dit->mod_a, dit->hidden, NULL, NULL,
+                           w->modulation, dit->row_map, rows, d, SLOTS, 3, 4,
+                           eps),
+                  "FFN adaLN") &&
+           dit_op(dit, h3_gpu_ffn_gelu_bf16(gpu, dit->proj, NULL, dit->mod_a,
+                                            w->fc1, w->fc1_bias, w->fc2,
+                                            w->fc2_bias, rows, d, c->ffn, d),
+                  "GELU FFN") &&
+           dit_op(dit, h3_gpu_gate_bf16(gpu, dit->hidden, dit->hidden,
+                                        dit->proj, w->modulation,
+                                        dit->row_map, rows, d, SLOTS, 5),
+                  "FFN gate");
+}
+
+int h3hip_dit_run_blocks(h3hip_dit *dit, uint32_t first, uint32_t count) {
+    if (!dit) return 0;
+    if (first > dit->config.blocks || count > dit->config.blocks - first)
+        return dit_fail(dit, "block range [%u, %u) outside %u blocks", first,
+                        first + count, dit->config.blocks);
+    dit->attention_adaln_ready = 0;
+    for (uint32_t b = first; b < first + count; b++) {
+        int ok = is_wan(dit) ? run_wan_block(dit, b)
+                             : run_h3_block(dit, b, b + 1 < first + count);
+        if (!ok) return 0;
+    }
+    return 1;
+}

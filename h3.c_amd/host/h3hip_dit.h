@@ -1,0 +1,94 @@
+/* DiT denoiser driver over the h3_gpu.h device API.
+ *
+ * Two block families share the same kernels:
+ *   H3HIP_FAMILY_H3  - the engine's MiniMax-H3 block (reference
+ *                      h3_dit.c:2008-2180): RMS adaLN, grouped QKV with
+ *                      per-head Q/K RMS norm and 3D RoPE, one joint
+ *                      self-attention over the packed sequence, SwiGLU MLP,
+ *                      gates fused with the next adaLN.
+ *   H3HIP_FAMILY_WAN - the Wan-style block the benchmark configs describe:
+ *                      LayerNorm adaLN, self-attention with per-head Q/K RMS
+ *                      norm and 3D RoPE, text cross-attention, GELU-tanh
+ *                      FFN, biases on every projection.
+ * All weights of all blocks stay resident in HBM.  The driver issues only
+ * h3_gpu.h / h3_hip.h calls; it never touches device memory itself.
+ */
+#ifndef H3HIP_DIT_H
+#define H3HIP_DIT_H
+
+#include "../../include/h3_gpu.h"
+#include "../../include/h3_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { H3HIP_FAMILY_H3 = 0, H3HIP_FAMILY_WAN = 1 };
+
+typedef struct {
+    int family;
+    uint32_t hidden;     /* H3: 5376, Wan: 5120 */
+    uint32_t heads;      /* H3: 56, Wan: 40 */
+    uint32_t head_dim;   /* 128 */
+    uint32_t ffn;        /* H3: 14336 (SwiGLU), Wan: 13824 (GELU) */
+    uint32_t blocks;     /* resident blocks (50) */
+    uint32_t rows;       /* H3: packed sequence; Wan: video rows */
+    uint32_t text_rows;  /* Wan: cross-attention context rows */
+    uint32_t time_rows;  /* modulation rows */
+    uint32_t rope_half;  /* 48 */
+    float epsilon;       /* 1e-5 for H3, 1e-6 for Wan */
+} h3hip_dit_config;
+
+typedef struct h3hip_dit h3hip_dit;
+
+/* Allocates every weight, modulation and activation tensor (uninitialised).
+ * Returns NULL and fills error on failure. */
+h3hip_dit *h3hip_dit_create(h3_gpu *gpu, const h3hip_dit_config *config,
+                            char *error, size_t error_size);
+void h3hip_dit_free(h3hip_dit *dit);
+
+/* Seeded device-side init: projection weights ~ N(0, weight_std^2), norm
+ * weights ~ 1 + N(0, 0.02^2), biases ~ N(0, 0.02^2), modulation
+ * ~ N(0, mod_std^2), hidden/context ~ N(0, 1).  Must be called outside a
+ * batch. */
+int h3hip_dit_init_random(h3hip_dit *dit, uint64_t seed, float weight_std,
+                          float mod_std);
+
+/* Upload RoPE tables ([rows][rope_half] F32 each; cast to bf16 with RNE on
+ * the device, as the reference does, h3_dit.c:960-1003) and the modulation
+ * row map ([rows] u32).  Outside a batch. */
+int h3hip_dit_set_rope(h3hip_dit *dit, const float *cosines,
+                       const float *sines);
+int h3hip_dit_set_row_map(h3hip_dit *dit, const uint32_t *row_map);
+
+/* Tensor handles, for tests and harnesses:
+ *   per block: "norm1" "norm2" "norm3" "norm3_bias" "qkv" "qkv_bias"
+ *              "q_norm" "k_norm" "out" "out_bias" "fc1" "fc1_bias" "fc2"
+ *              "fc2_bias" "cq" "cq_bias" "ck" "ck_bias" "cv" "cv_bias"
+ *              "cq_norm" "ck_norm" "co" "co_bias" "modulation"
+ *   shared (block ignored): "hidden" "row_map" "rope_cos" "rope_sin"
+ *              "context"
+ * Returns NULL for a name the family does not use. */
+h3_gpu_tensor *h3hip_dit_tensor(h3hip_dit *dit, const char *name,
+                                uint32_t block);
+
+/* Run blocks [first, first + count) on the current hidden state inside an
+ * open batch (h3_gpu_begin .. h3_gpu_submit is the caller's).  For H3, the
+ * MLP gate of a block is fused with the next block's attention adaLN when
+ * the next block is in the range (reference h3_dit.c:2139-2178). */
+int h3hip_dit_run_blocks(h3hip_dit *dit, uint32_t first, uint32_t count);
+
+/* Algorithmic FLOPs of one block at the configured shape (GEMMs + attention,
+ * 2 flops per multiply-add). */
+double h3hip_dit_block_flops(const h3hip_dit_config *config);
+/* FLOPs of the GEMMs alone and of the attention alone. */
+double h3hip_dit_block_gemm_flops(const h3hip_dit_config *config);
+double h3hip_dit_block_attention_flops(const h3hip_dit_config *config);
+
+const char *h3hip_dit_error(const h3hip_dit *dit);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,118 @@
+/* h3_hip.h - entry points of the MI355X HIP backend that the reference
+ * device API (h3_gpu.h) does not have.
+ *
+ * None of these replaces a reference symbol.  They exist for three reasons:
+ *   1. the backend probe that the engine selects per build
+ *      (h3_hip_probe, counterpart of h3_cuda_probe, reference
+ *      h3_cuda.h:6-8 and h3_gpu_cuda.cu:47-79);
+ *   2. the ops a Wan-style DiT block needs and h3_gpu.h lacks: attention
+ *      with q_rows != kv_rows, LayerNorm adaLN, a GELU-tanh FFN
+ *      (the GELU formula is the reference's h3_cuda_core.cu:139-158);
+ *   3. device-side seeded initialisation and per-op timing for the
+ *      benchmark harness.
+ * Same conventions as h3_gpu.h: 1 = success, 0 = failure + h3_gpu_error().
+ */
+#ifndef H3_HIP_H
+#define H3_HIP_H
+
+#include "h3_gpu.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Field-for-field layout of the engine's h3_device_info
+ * (reference h3.h:137-146), so a build can alias the two. */
+struct h3_hip_device_info {
+    char name[128];
+    char architecture[128];
+    uint64_t physical_memory;
+    uint64_t recommended_working_set;
+    uint64_t max_buffer_length;
+    int apple_gpu_family;
+    int metal4;
+    int unified_memory;
+};
+
+int h3_hip_probe(struct h3_hip_device_info *info, char *error,
+                 size_t error_size);
+
+/* Cross attention: Q [q_rows][heads][head_dim] against K/V
+ * [kv_rows][heads][head_dim]; output [q_rows][heads][head_dim].  Same
+ * numerics as h3_gpu_sdpa_bf16 (F32 online softmax, P rounded to bf16
+ * before P.V). */
+int h3_gpu_sdpa_cross_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                           const h3_gpu_tensor *query,
+                           const h3_gpu_tensor *key,
+                           const h3_gpu_tensor *value, uint32_t q_rows,
+                           uint32_t kv_rows, uint32_t heads,
+                           uint32_t head_dim, float scale);
+
+/* LayerNorm adaLN:
+ *   n = (x - mean) * rsqrt(var + eps) [* w + b]      (w, b may be NULL)
+ *   y = bf16(n * (1 + mod[scale]) + mod[shift])
+ * with the modulation row chosen per token by row_map, as in
+ * h3_gpu_adaln_bf16.  A NULL modulation (and row_map) gives a plain
+ * LayerNorm. */
+int h3_gpu_layer_adaln_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                            const h3_gpu_tensor *input,
+                            const h3_gpu_tensor *norm_weight,
+                            const h3_gpu_tensor *norm_bias,
+                            const h3_gpu_tensor *modulation,
+                            const h3_gpu_tensor *row_map, uint32_t rows,
+                            uint32_t width, uint32_t slots,
+                            uint32_t shift_slot, uint32_t scale_slot,
+                            float epsilon);
+
+/* output = bf16(gelu_tanh(bf16(X . W^T + b))): GEMM with the activation in
+ * its epilogue. */
+int h3_gpu_linear_gelu_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                            const h3_gpu_tensor *input,
+                            const h3_gpu_tensor *weight,
+                            const h3_gpu_tensor *bias, uint32_t rows,
+                            uint32_t input_dim, uint32_t output_dim);
+
+/* Non-gated GELU-tanh FFN: fc2(gelu(fc1(x) + b1)) + b2.  activated is
+ * caller-owned scratch of rows*hidden_dim bf16, or NULL to use the
+ * context's workspace.  Biases may be NULL. */
+int h3_gpu_ffn_gelu_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                         h3_gpu_tensor *activated,
+                         const h3_gpu_tensor *input,
+                         const h3_gpu_tensor *fc1_weight,
+                         const h3_gpu_tensor *fc1_bias,
+                         const h3_gpu_tensor *fc2_weight,
+                         const h3_gpu_tensor *fc2_bias, uint32_t rows,
+                         uint32_t input_dim, uint32_t hidden_dim,
+                         uint32_t output_dim);
+
+/* Seeded N(mean, stddev^2) fill of elements values starting at offset,
+ * generated on the device (counter-based: value i depends only on seed and
+ * i).  Used to initialise resident random weights without host uploads. */
+int h3_gpu_fill_normal_bf16(h3_gpu *gpu, h3_gpu_tensor *tensor,
+                            size_t offset, size_t elements, uint64_t seed,
+                            float mean, float stddev);
+int h3_gpu_fill_normal_f32(h3_gpu *gpu, h3_gpu_tensor *tensor,
+                           size_t offset, size_t elements, uint64_t seed,
+                           float mean, float stddev);
+
+/* Per-op device timing.  While enabled, every launch is bracketed by a pair
+ * of HIP events on the context's stream; h3_hip_op_timing_read() waits for
+ * the stream and returns the number of launches and their summed device
+ * milliseconds for the ops whose name starts with prefix ("" = all). */
+int h3_hip_op_timing_enable(h3_gpu *gpu, int enable);
+int h3_hip_op_timing_reset(h3_gpu *gpu);
+int h3_hip_op_timing_read(h3_gpu *gpu, const char *prefix,
+                          uint64_t *count, double *milliseconds);
+/* Names of the distinct timed ops, '\n'-separated, into buffer. */
+int h3_hip_op_timing_names(h3_gpu *gpu, char *buffer, size_t buffer_size);
+
+/* Device milliseconds between two markers recorded on the context stream. */
+int h3_hip_marker(h3_gpu *gpu, int slot);
+int h3_hip_marker_elapsed(h3_gpu *gpu, int from_slot, int to_slot,
+                          double *milliseconds);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,408 @@
+"""Per-op parity of the HIP backend against the CPU oracle, through the C ABI.
+
+Mirrors the reference's synthetic op tests (tests/test_cuda_dit.c,
+tests/test_cuda_attention.c, tests/test_cuda_core.c): seeded inputs, an
+independent CPU statement of each op, and the reference's tolerances --
+bit-exact or one bf16 ulp for the row/elementwise ops, 1e-3 abs + 1e-2 rel
+for GEMM and flash attention.
+"""
+import ctypes as C
+import math
+
+import numpy as np
+import pytest
+
+from conftest import (adaln_terms, assert_close, assert_row_close,
+                      assert_ulp, rand_bf16, to_f32)
+
+pytestmark = pytest.mark.gpu
+
+import oracle  # noqa: E402
+
+
+def _mod_setup(rng, rows, width, slots=6, mod_rows=4):
+    mod = rand_bf16(rng, mod_rows * slots * width, 0.5)
+    row_map = rng.integers(0, mod_rows, rows).astype(np.uint32)
+    return mod, row_map
+
+
+# ------------------------------------------------------------------ GEMM
+
+@pytest.mark.parametrize("m,k,n,bias", [
+    (32, 256, 256, False),      # reference test_cuda_core.c linear shape
+    (100, 512, 768, True),      # ragged M
+    (1, 256, 512, False),       # single row
+    (300, 5376, 1024, False),   # real K (hidden)
+    (257, 1024, 1280, True),    # M just past a tile
+    (64, 96, 256, True),        # K % 64 != 0 -> sequential fallback kernel
+])
+def test_linear_bf16(gpu, m, k, n, bias):
+    rng = np.random.default_rng(m * 7 + k + n)
+    x = rand_bf16(rng, m * k)
+    w = rand_bf16(rng, n * k, 0.05)
+    b = rand_bf16(rng, n, 0.1) if bias else None
+    want = oracle.linear(x, w, b, m, k, n)
+    tx, tw, to = gpu.bf16(x), gpu.bf16(w), gpu.new_bf16(m * n)
+    tb = gpu.bf16(b) if bias else None
+    gpu.run("h3_gpu_linear_bf16", to, tx, tw, tb, m, k, n)
+    got = gpu.read_bf16(to)
+    assert_close(got, want, what=f"linear {m}x{k}x{n}")
+
+
+def test_linear_stats_kind(gpu):
+    """Routing-shape rule of the stats counters (reference
+    h3_cuda_core.cu:838-841): rows >= 32, in >= 256, out >= 256 -> kind 1."""
+    rng = np.random.default_rng(1)
+    before = gpu.stats().mps_linear_dispatches
+    x, w = gpu.bf16(rand_bf16(rng, 32 * 256)), gpu.bf16(rand_bf16(rng, 256 * 256))
+    gpu.run("h3_gpu_linear_bf16", gpu.new_bf16(32 * 256), x, w, None, 32, 256,
+            256)
+    assert gpu.stats().mps_linear_dispatches == before + 1
+
+
+@pytest.mark.parametrize("rows,d,ffn", [(64, 256, 512), (300, 1024, 1536),
+                                        (130, 5376, 512)])
+def test_mlp_swiglu(gpu, rows, d, ffn):
+    rng = np.random.default_rng(rows + d + ffn)
+    x = rand_bf16(rng, rows * d)
+    fc1 = rand_bf16(rng, 2 * ffn * d, 0.04)
+    fc2 = rand_bf16(rng, d * ffn, 0.04)
+    want = oracle.mlp(x, fc1, fc2, rows, d, ffn)
+    out = gpu.new_bf16(rows * d)
+    gpu.run("h3_gpu_mlp_bf16", out, gpu.bf16(x), gpu.bf16(fc1), gpu.bf16(fc2),
+            rows, d, ffn, d)
+    assert_close(gpu.read_bf16(out), want, what="SwiGLU MLP", chained=1)
+
+
+def test_ffn_gelu(gpu):
+    rows, d, ffn = 200, 512, 768
+    rng = np.random.default_rng(5)
+    x = rand_bf16(rng, rows * d)
+    fc1, b1 = rand_bf16(rng, ffn * d, 0.05), rand_bf16(rng, ffn, 0.1)
+    fc2, b2 = rand_bf16(rng, d * ffn, 0.05), rand_bf16(rng, d, 0.1)
+    want = oracle.ffn_gelu(x, fc1, b1, fc2, b2, rows, d, ffn)
+    out = gpu.new_bf16(rows * d)
+    gpu.run("h3_gpu_ffn_gelu_bf16", out, None, gpu.bf16(x), gpu.bf16(fc1),
+            gpu.bf16(b1), gpu.bf16(fc2), gpu.bf16(b2), rows, d, ffn, d)
+    assert_close(gpu.read_bf16(out), want, what="GELU FFN", chained=1)
+
+
+# ------------------------------------------------------------- row ops
+
+WIDTHS = [8, 100, 5120, 5376]
+
+
+@pytest.mark.parametrize("width", WIDTHS)
+def test_adaln(gpu, width):
+    rows = 37
+    rng = np.random.default_rng(width)
+    x = rand_bf16(rng, rows * width, 2.0)
+    w = rand_bf16(rng, width, 0.1, 1.0)
+    mod, rm = _mod_setup(rng, rows, width)
+    want = oracle.adaln(x, w, mod, rm, rows, width, 6, 0, 1, 1e-5)
+    out = gpu.new_bf16(rows * width)
+    gpu.run("h3_gpu_adaln_bf16", out, gpu.bf16(x), gpu.bf16(w), gpu.bf16(mod),
+            gpu.u32(rm), rows, width, 6, 0, 1, C.c_float(1e-5))
+    assert_row_close(gpu.read_bf16(out), want,
+                     adaln_terms(x, w, mod, rm, rows, width, 6, 0, 1, 1e-5),
+                     "adaLN")
+
+
+def test_adaln_offset(gpu):
+    rows, width, off_rows = 5, 5376, 3
+    rng = np.random.default_rng(9)
+    x = rand_bf16(rng, (rows + off_rows) * width)
+    w = rand_bf16(rng, width, 0.1, 1.0)
+    mod, rm = _mod_setup(rng, rows, width)
+    want = oracle.adaln(x[off_rows * width:], w, mod, rm, rows, width, 6, 3, 4,
+                        1e-5)
+    out = gpu.new_bf16(rows * width)
+    gpu.run("h3_gpu_adaln_bf16_offset", out, gpu.bf16(x), off_rows * width,
+            gpu.bf16(w), gpu.bf16(mod), gpu.u32(rm), rows, width, 6, 3, 4,
+            C.c_float(1e-5))
+    assert_row_close(gpu.read_bf16(out), want,
+                     adaln_terms(x[off_rows * width:], w, mod, rm, rows,
+                                 width, 6, 3, 4, 1e-5), "adaLN offset")
+
+
+@pytest.mark.parametrize("width", WIDTHS)
+def test_gate(gpu, width):
+    rows = 29
+    rng = np.random.default_rng(width + 1)
+    res, br = rand_bf16(rng, rows * width), rand_bf16(rng, rows * width)
+    mod, rm = _mod_setup(rng, rows, width)
+    want = oracle.gate(res, br, mod, rm, rows, width, 6, 2)
+    out = gpu.new_bf16(rows * width)
+    gpu.run("h3_gpu_gate_bf16", out, gpu.bf16(res), gpu.bf16(br),
+            gpu.bf16(mod), gpu.u32(rm), rows, width, 6, 2)
+    assert_ulp(gpu.read_bf16(out), want, 0, "gate (bit-exact)")
+
+
+@pytest.mark.parametrize("width", WIDTHS)
+def test_gate_adaln(gpu, width):
+    rows = 31
+    rng = np.random.default_rng(width + 2)
+    res, br = rand_bf16(rng, rows * width), rand_bf16(rng, rows * width)
+    w = rand_bf16(rng, width, 0.1, 1.0)
+    gmod, rm = _mod_setup(rng, rows, width)
+    nmod = rand_bf16(rng, gmod.size, 0.5)
+    gated_want, want = oracle.gate_adaln(res, br, w, gmod, nmod, rm, rows,
+                                         width, 6, 5, 0, 1, 1e-5)
+    gated, out = gpu.new_bf16(rows * width), gpu.new_bf16(rows * width)
+    gpu.run("h3_gpu_gate_adaln_bf16", gated, out, gpu.bf16(res), gpu.bf16(br),
+            gpu.bf16(w), gpu.bf16(gmod), gpu.bf16(nmod), gpu.u32(rm), rows,
+            width, 6, 5, 0, 1, C.c_float(1e-5))
+    assert_ulp(gpu.read_bf16(gated), gated_want, 0, "gated residual")
+    assert_row_close(gpu.read_bf16(out), want,
+                     adaln_terms(gated_want, w, nmod, rm, rows, width, 6, 0,
+                                 1, 1e-5), "gate+adaLN")
+
+
+def test_gate_adaln_in_place(gpu):
+    """The driver passes hidden as both residual and gated output."""
+    rows, width = 17, 5376
+    rng = np.random.default_rng(77)
+    res, br = rand_bf16(rng, rows * width), rand_bf16(rng, rows * width)
+    w = rand_bf16(rng, width, 0.1, 1.0)
+    mod, rm = _mod_setup(rng, rows, width)
+    gated_want, want = oracle.gate_adaln(res, br, w, mod, mod, rm, rows,
+                                         width, 6, 2, 3, 4, 1e-5)
+    hidden, out = gpu.bf16(res), gpu.new_bf16(rows * width)
+    tmod = gpu.bf16(mod)
+    gpu.run("h3_gpu_gate_adaln_bf16", hidden, out, hidden, gpu.bf16(br),
+            gpu.bf16(w), tmod, tmod, gpu.u32(rm), rows, width, 6, 2, 3, 4,
+            C.c_float(1e-5))
+    assert_ulp(gpu.read_bf16(hidden), gated_want, 0, "in-place gated")
+    assert_row_close(gpu.read_bf16(out), want,
+                     adaln_terms(gated_want, w, mod, rm, rows, width, 6, 3, 4,
+                                 1e-5), "in-place gate+adaLN")
+
+
+@pytest.mark.parametrize("width", [8, 100, 5120])
+@pytest.mark.parametrize("affine,modulated", [(False, True), (True, False),
+                                              (True, True)])
+def test_layer_adaln(gpu, width, affine, modulated):
+    rows = 23
+    rng = np.random.default_rng(width * 3 + affine + 2 * modulated)
+    x = rand_bf16(rng, rows * width, 3.0, 0.5)
+    w = rand_bf16(rng, width, 0.1, 1.0) if affine else None
+    b = rand_bf16(rng, width, 0.1) if affine else None
+    mod, rm = _mod_setup(rng, rows, width) if modulated else (None, None)
+    want = oracle.layer_adaln(x, w, b, mod, rm, rows, width, 6, 0, 1, 1e-6)
+    out = gpu.new_bf16(rows * width)
+    gpu.run("h3_gpu_layer_adaln_bf16", out, gpu.bf16(x),
+            gpu.bf16(w) if affine else None, gpu.bf16(b) if affine else None,
+            gpu.bf16(mod) if modulated else None,
+            gpu.u32(rm) if modulated else None, rows, width, 6, 0, 1,
+            C.c_float(1e-6))
+    assert_row_close(gpu.read_bf16(out), want,
+                     adaln_terms(x, w, mod, rm, rows, width, 6, 0, 1, 1e-6,
+                                 layer=True, bias=b), "LayerNorm adaLN")
+
+
+@pytest.mark.parametrize("width", [8, 5376])
+def test_rms_norm(gpu, width):
+    rows = 9
+    rng = np.random.default_rng(width + 3)
+    x, w = rand_bf16(rng, rows * width), rand_bf16(rng, width, 0.1, 1.0)
+    want = oracle.rms_norm(x, w, rows, width, 1e-5)
+    out = gpu.new_bf16(rows * width)
+    gpu.run("h3_gpu_rms_norm_bf16", out, gpu.bf16(x), gpu.bf16(w), rows, width,
+            C.c_float(1e-5))
+    assert_row_close(gpu.read_bf16(out), want,
+                     adaln_terms(x, w, None, None, rows, width, 6, 0, 0,
+                                 1e-5), "RMS norm")
+
+
+def test_head_rms_norm(gpu):
+    rows, heads, hd = 33, 5, 128
+    rng = np.random.default_rng(11)
+    x, w = rand_bf16(rng, rows * heads * hd), rand_bf16(rng, hd, 0.1, 1.0)
+    want = oracle.head_rms_norm(x, w, rows, heads, hd, 1e-6)
+    t = gpu.bf16(x)
+    gpu.run("h3_gpu_head_rms_norm_bf16", t, gpu.bf16(w), rows, heads, hd,
+            C.c_float(1e-6))
+    assert_ulp(gpu.read_bf16(t), want, 1, "head RMS norm")
+
+
+@pytest.mark.parametrize("grouped", [True, False])
+@pytest.mark.parametrize("hd,rope_half", [(128, 48), (64, 16)])
+def test_qkv_rope(gpu, grouped, hd, rope_half):
+    seq, heads = 45, 3
+    rng = np.random.default_rng(hd + rope_half + grouped)
+    qkv = rand_bf16(rng, seq * 3 * heads * hd)
+    qw, kw = rand_bf16(rng, hd, 0.1, 1.0), rand_bf16(rng, hd, 0.1, 1.0)
+    ang = rng.uniform(-30, 30, seq * rope_half).astype(np.float32)
+    cos, sin = oracle.bf16(np.cos(ang)), oracle.bf16(np.sin(ang))
+    q, k, v = oracle.qkv_rope(qkv, qw, kw, cos, sin, seq, heads, hd,
+                              rope_half, grouped, 1e-5)
+    n = seq * heads * hd
+    tq, tk, tv = gpu.new_bf16(n), gpu.new_bf16(n), gpu.new_bf16(n)
+    name = ("h3_gpu_grouped_qkv_rope_bf16" if grouped
+            else "h3_gpu_qkv_rope_bf16")
+    gpu.run(name, tq, tk, tv, gpu.bf16(qkv), gpu.bf16(qw), gpu.bf16(kw),
+            gpu.bf16(cos), gpu.bf16(sin), seq, heads, hd, rope_half,
+            C.c_float(1e-5))
+    assert_ulp(gpu.read_bf16(tq), q, 1, "query")
+    assert_ulp(gpu.read_bf16(tk), k, 1, "key")
+    assert_ulp(gpu.read_bf16(tv), v, 0, "value copy")
+
+
+# ------------------------------------------------------------ attention
+
+@pytest.mark.parametrize("q_rows,kv_rows,heads", [
+    (100, 100, 2),      # reference test_cuda_attention.c hd128 N=100
+    (300, 300, 3),      # two 256-query blocks, ragged key tail
+    (64, 64, 1),        # exactly one key tile
+    (1000, 1000, 2),
+    (300, 77, 2),       # cross attention, short context
+    (70, 513, 2),       # cross attention, more keys than queries
+])
+def test_sdpa(gpu, q_rows, kv_rows, heads):
+    hd = 128
+    rng = np.random.default_rng(q_rows * 3 + kv_rows)
+    q = rand_bf16(rng, q_rows * heads * hd)
+    k = rand_bf16(rng, kv_rows * heads * hd)
+    v = rand_bf16(rng, kv_rows * heads * hd)
+    scale = 1.0 / math.sqrt(hd)
+    want = oracle.sdpa(q, k, v, q_rows, kv_rows, heads, hd, scale)
+    out = gpu.new_bf16(q_rows * heads * hd)
+    if q_rows == kv_rows:
+        gpu.run("h3_gpu_sdpa_bf16", out, gpu.bf16(q), gpu.bf16(k), gpu.bf16(v),
+                q_rows, heads, hd, C.c_float(scale))
+    else:
+        gpu.run("h3_gpu_sdpa_cross_bf16", out, gpu.bf16(q), gpu.bf16(k),
+                gpu.bf16(v), q_rows, kv_rows, heads, hd, C.c_float(scale))
+    assert_close(gpu.read_bf16(out), want, what=f"SDPA {q_rows}x{kv_rows}")
+
+
+def test_sdpa_head_major(gpu):
+    n, heads, hd = 150, 2, 128
+    rng = np.random.default_rng(21)
+    q, k, v = (rand_bf16(rng, n * heads * hd) for _ in range(3))
+    scale = 1.0 / math.sqrt(hd)
+    want = oracle.sdpa(q, k, v, n, n, heads, hd, scale, head_major=True)
+    out = gpu.new_bf16(n * heads * hd)
+    gpu.run("h3_gpu_sdpa_bf16_head_major_output", out, gpu.bf16(q),
+            gpu.bf16(k), gpu.bf16(v), n, heads, hd, C.c_float(scale))
+    assert_close(gpu.read_bf16(out), want, what="head-major SDPA")
+
+
+def test_sdpa_constant_keys_give_mean_value(gpu):
+    """Invariant: identical keys -> uniform softmax -> output = mean of V."""
+    n, heads, hd = 200, 1, 128
+    rng = np.random.default_rng(3)
+    q = rand_bf16(rng, n * heads * hd)
+    k = np.tile(rand_bf16(rng, hd), n)
+    vf = rng.standard_normal((n, hd)).astype(np.float32)
+    v = oracle.bf16(vf)
+    out = gpu.new_bf16(n * hd)
+    gpu.run("h3_gpu_sdpa_bf16", out, gpu.bf16(q), gpu.bf16(k), gpu.bf16(v), n,
+            heads, hd, C.c_float(1.0 / math.sqrt(hd)))
+    got = to_f32(gpu.read_bf16(out)).reshape(n, hd)
+    mean = to_f32(v).reshape(n, hd).astype(np.float64).mean(axis=0)
+    np.testing.assert_allclose(got, np.broadcast_to(mean, got.shape),
+                               atol=2e-2, rtol=2e-2)
+
+
+# --------------------------------------------------------- elementwise
+
+def test_swiglu_gelu_add_sub(gpu):
+    rows, width = 13, 300
+    rng = np.random.default_rng(4)
+    fused = rand_bf16(rng, rows * 2 * width, 3.0)
+    out = gpu.new_bf16(rows * width)
+    gpu.run("h3_gpu_swiglu_bf16", out, gpu.bf16(fused), rows, width)
+    assert_ulp(gpu.read_bf16(out), oracle.swiglu(fused, rows, width), 1,
+               "SwiGLU")
+    x = rand_bf16(rng, 5000, 4.0)
+    out = gpu.new_bf16(x.size)
+    gpu.run("h3_gpu_gelu_bf16", out, gpu.bf16(x), x.size, 1)
+    assert_ulp(gpu.read_bf16(out), oracle.gelu(x), 1, "GELU tanh")
+    y = rand_bf16(rng, 5000)
+    gpu.run("h3_gpu_add_bf16", out, gpu.bf16(x), gpu.bf16(y), x.size)
+    assert_ulp(gpu.read_bf16(out), oracle.add(x, y), 0, "add")
+
+
+def test_euler_step(gpu):
+    n = 4099
+    rng = np.random.default_rng(8)
+    sample = rng.standard_normal(n + 10).astype(np.float32)
+    last, prev = rand_bf16(rng, n), rand_bf16(rng, n)
+    delta, ratio = 0.0625, -0.5
+    want = sample.copy()
+    want[10:] = oracle.euler(sample[10:], last, prev, delta, ratio)
+    t = gpu.f32(sample)
+    gpu.run("h3_gpu_euler_bf16", t, 10, gpu.bf16(last), gpu.bf16(prev), n,
+            C.c_float(delta), C.c_float(ratio))
+    np.testing.assert_array_equal(gpu.read_f32(t), want)
+
+
+def test_final_adaln_head(gpu):
+    rows, width, n, slots = 20, 5376, 96, 2
+    rng = np.random.default_rng(12)
+    x = rand_bf16(rng, (rows + 4) * width)
+    nw = rand_bf16(rng, width, 0.1, 1.0)
+    mod, rm = _mod_setup(rng, rows, width, slots=slots, mod_rows=2)
+    w, b = rand_bf16(rng, n * width, 0.02), rand_bf16(rng, n, 0.1)
+    want, inv_want = oracle.adaln_linear(x[4 * width:], nw, mod, rm, w, b,
+                                         rows, width, n, slots, 0, 1, 1e-5)
+    out, inv = gpu.new_bf16(rows * n), gpu.new_f32(rows)
+    gpu.run("h3_gpu_adaln_linear_bf16", out, inv, gpu.bf16(x), 4 * width,
+            gpu.bf16(nw), gpu.bf16(mod), gpu.u32(rm), gpu.bf16(w), gpu.bf16(b),
+            rows, width, n, slots, 0, 1, C.c_float(1e-5))
+    np.testing.assert_allclose(gpu.read_f32(inv), inv_want, rtol=1e-5)
+    assert_close(gpu.read_bf16(out), want, what="final head", chained=1)
+
+
+def test_patch_linear_bit_exact(gpu):
+    """F32 patch projection keeps the reference hand kernel's sequential
+    order, so it matches the oracle bit for bit."""
+    rows, k, n = 40, 96, 5376
+    rng = np.random.default_rng(13)
+    x = rng.standard_normal(rows * k).astype(np.float32)
+    w = (0.05 * rng.standard_normal(n * k)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(n)).astype(np.float32)
+    out_rows = 50
+    rm = rng.permutation(out_rows)[:rows].astype(np.uint32)
+    want = oracle.patch_linear(x, w, b, rows, k, n, row_map=rm,
+                               out_rows=out_rows)
+    out = gpu.bf16(np.zeros(out_rows * n, np.uint16))
+    gpu.run("h3_gpu_patch_linear_bf16_map", out, gpu.f32(x), gpu.f32(w),
+            gpu.f32(b), gpu.u32(rm), out_rows, rows, k, n)
+    assert_ulp(gpu.read_bf16(out), want, 0, "mapped patch projection")
+
+
+# ------------------------------------------------------------ contract
+
+def test_ops_require_an_open_batch(gpu):
+    t = gpu.new_bf16(16)
+    ok = gpu.L.h3_gpu_add_bf16(gpu.h, t, t, t, 16)
+    assert ok == 0 and "no active command buffer" in gpu.error()
+
+
+def test_validation_errors(gpu):
+    rng = np.random.default_rng(0)
+    x = gpu.bf16(rand_bf16(rng, 64))
+    f = gpu.new_f32(64)
+    gpu.begin()
+    try:
+        assert gpu.L.h3_gpu_add_bf16(gpu.h, f, x, x, 64) == 0
+        assert "wrong dtype" in gpu.error()
+        assert gpu.L.h3_gpu_add_bf16(gpu.h, x, x, x, 65) == 0
+        assert "too small" in gpu.error()
+        mod, rm = gpu.bf16(rand_bf16(rng, 6 * 8)), gpu.u32(np.zeros(8, np.uint32))
+        assert gpu.L.h3_gpu_gate_bf16(gpu.h, x, x, x, mod, rm, 8, 8, 6,
+                                      6) == 0
+        assert "slot" in gpu.error()
+        assert gpu.L.h3_gpu_gate_adaln_bf16(
+            gpu.h, x, x, x, x, x, mod, mod, rm, 1, 6000, 6, 2, 3, 4,
+            C.c_float(1e-5)) == 0
+        assert "out of range" in gpu.error()
+    finally:
+        gpu.L.h3_gpu_submit(gpu.h)
+
+
+def test_int8_paths_report_unavailable(gpu):
+    assert gpu.L.h3_gpu_has_int8_mlp(gpu.h) == 0
+    assert gpu.L.h3_gpu_prefers_gpu_sampler(gpu.h) == 1
