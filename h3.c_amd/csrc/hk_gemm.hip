@@ -41,9 +41,11 @@
 #define HK_BM 256
 #define HK_BN 256
 #define HK_BK 64
+#define HK_STAGES 2
 #define HK_GEMM_THREADS 256
-#define HK_TILE_BYTES (HK_BM * HK_BK * 2) /* 32 KiB per operand per stage */
-#define HK_GEMM_LDS (4 * HK_TILE_BYTES)   /* 2 stages x 2 operands */
+#define HK_TILE_BYTES (HK_BM * HK_BK * 2)       /* 32 KiB per operand */
+#define HK_STAGE_BYTES (2 * HK_TILE_BYTES)      /* X tile then W tile */
+#define HK_GEMM_LDS (HK_STAGES * HK_STAGE_BYTES) /* 128 KiB */
 #define HK_GROUP_M 8
 
 typedef int hk_v4i __attribute__((ext_vector_type(4)));
@@ -55,20 +57,35 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t hk_rsrc(const void *base,
                                              0x00020000);
 }
 
-/* byte offset of 16-byte chunk `chunk` of LDS row `row` */
-__device__ __forceinline__ uint32_t hk_swz(uint32_t row, uint32_t chunk) {
-    return row * 128u + ((chunk ^ (row & 7u)) << 4);
+/* LDS rows are 128 B (64 bf16 = 8 chunks of 16 B); logical chunk c of row
+ * r lives at physical chunk c ^ key(r).  Any 8 consecutive rows get
+ * distinct keys (32-bank view, 128 B per cycle) and any 16 consecutive rows
+ * distinct (r & 1, key) pairs (64-bank view, 256 B per cycle), so the
+ * 32-row fragment reads are conflict-free under either bank model. */
+__device__ __forceinline__ uint32_t hk_swz_key(uint32_t row) {
+    return (row & 7u) ^ ((row >> 3) & 1u);
+}
+
+/* Epilogue activations from the hardware exp2/rcp (v_exp_f32, v_rcp_f32,
+ * about 1 ulp each): silu(x) = x / (1 + e^-x) and the reference's tanh-form
+ * GELU with its +-10 saturation (h3_cuda_core.cu:139-158), using
+ * tanh(u) = 1 - 2 / (e^(2u) + 1).  Their f32 error is far below half a
+ * bf16 ulp, the rounding applied right after. */
+__device__ __forceinline__ float hk_exp_fast(float x) {
+    return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }
 
 __device__ __forceinline__ float hk_silu_f(float x) {
-    return x / (1.0f + expf(-x));
+    return x * __builtin_amdgcn_rcpf(1.0f + hk_exp_fast(-x));
 }
 
 __device__ __forceinline__ float hk_gelu_tanh_f(float x) {
     float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+    float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(hk_exp_fast(2.0f * inner) +
+                                                  1.0f);
     return inner <= -10.0f ? 0.0f
          : inner >= 10.0f  ? x
-                           : 0.5f * x * (1.0f + tanhf(inner));
+                           : 0.5f * x * (1.0f + t);
 }
 
 struct hk_gemm_args {
@@ -83,6 +100,7 @@ struct hk_gemm_args {
 
 template <int EPI>
 __global__ void __launch_bounds__(HK_GEMM_THREADS, 1)
+__attribute__((amdgpu_waves_per_eu(1, 1)))
 hk_gemm_mfma(hk_gemm_args g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t hk_smem[];
     const uint32_t tid = threadIdx.x;
@@ -101,30 +119,34 @@ hk_gemm_mfma(hk_gemm_args g) {
     const uint32_t tile_n = in_band / band_rows;
     const uint32_t m0 = tile_m * HK_BM;
 
-    /* ---- per-thread load plan: 8 chunks of X rows and of W rows ---- */
+    /* ---- staging plan ----
+     * Each operand tile is 256 rows x 8 chunks (16 B) = 2048 chunks per
+     * stage.  Direct-to-LDS buffer loads write lane i of a wave to LDS byte
+     * base + 16 i, so the swizzle is applied on the global side: wave w,
+     * load j covers LDS chunk slots p = (8 w + j) * 64 + lane, i.e. row
+     * p / 8, physical chunk p % 8, holding logical chunk (p % 8) ^ key(row).
+     * Rows past M (and W rows past the end) get an offset beyond the
+     * buffer, which the hardware returns as zeros. */
     const __amdgpu_buffer_rsrc_t xr = hk_rsrc(g.x, g.x_bytes);
     const __amdgpu_buffer_rsrc_t wr = hk_rsrc(g.w, g.w_bytes);
-    const uint32_t lc = tid & 7u;   /* chunk within the 64-k row slice */
-    const uint32_t lr = tid >> 3;   /* rows lr + 32 i */
     uint32_t x_off[8], w_off[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const uint32_t row = lr + 32u * i;
-        /* rows past M: offset beyond the buffer -> zeros */
-        const uint32_t xm = m0 + row;
-        x_off[i] = xm < g.m ? (xm * g.k + lc * 8u) * 2u : 0xfffffff0u;
+    for (int j = 0; j < 8; j++) {
+        const uint32_t slot = (wave * 8u + j) * 64u + lane;
+        const uint32_t row = slot >> 3;
+        const uint32_t chunk = (slot & 7u) ^ hk_swz_key(row);
+        const uint32_t xm = min(m0 + row, g.m);
+        x_off[j] = xm * g.k * 2u + chunk * 16u;
         uint32_t wrow;
         if (EPI == HK_EPI_SWIGLU) {
             /* W tile rows: per wave half 64 gate rows then 64 up rows */
             const uint32_t half = row >> 7, within = row & 127u;
             const uint32_t col = tile_n * 128u + half * 64u + (within & 63u);
-            wrow = col < g.n ? (within >> 6) * g.n + col : 0xffffffffu;
+            wrow = col < g.n ? (within >> 6) * g.n + col : 2u * g.n;
         } else {
-            wrow = tile_n * HK_BN + row;
-            if (wrow >= g.n) wrow = 0xffffffffu;
+            wrow = min(tile_n * HK_BN + row, g.n);
         }
-        w_off[i] = wrow != 0xffffffffu ? (wrow * g.k + lc * 8u) * 2u
-                                       : 0xfffffff0u;
+        w_off[j] = wrow * g.k * 2u + chunk * 16u;
     }
 
     hk_f32x16 acc[4][4];
@@ -135,61 +157,117 @@ hk_gemm_mfma(hk_gemm_args g) {
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
-    hk_v4i xs[8], ws[8];
-    auto load_global = [&](uint32_t k0) {
+    auto issue_loads = [&](uint32_t stage, uint32_t k0) {
+        uint8_t *sx = hk_smem + stage * HK_STAGE_BYTES;
+        uint8_t *sw = sx + HK_TILE_BYTES;
         const uint32_t kb = k0 * 2u;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            xs[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                xr, x_off[i] == 0xfffffff0u ? x_off[i] : x_off[i] + kb, 0, 0);
-            ws[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                wr, w_off[i] == 0xfffffff0u ? w_off[i] : w_off[i] + kb, 0, 0);
-        }
-    };
-    auto store_lds = [&](uint32_t stage) {
-        uint8_t *sx = hk_smem + stage * (2 * HK_TILE_BYTES);
-        uint8_t *sw = sx + HK_TILE_BYTES;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const uint32_t row = lr + 32u * i;
-            *(hk_v4i *)(sx + hk_swz(row, lc)) = xs[i];
-            *(hk_v4i *)(sw + hk_swz(row, lc)) = ws[i];
+        for (int j = 0; j < 8; j++) {
+            const uint32_t base = (wave * 8u + j) * 1024u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                xr, (__attribute__((address_space(3))) void *)(sx + base), 16,
+                x_off[j] + kb, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                wr, (__attribute__((address_space(3))) void *)(sw + base), 16,
+                w_off[j] + kb, 0, 0, 0);
         }
     };
 
+    /* ---- main loop ----
+     * Fragments are read with inline ds_read_b128 one k-step ahead of the
+     * MFMAs that consume them; the matching s_waitcnt names the fragment
+     * registers as operands, and sched_barrier(0) pins the read / MFMA /
+     * wait phases so the scheduler cannot fold them back together.  The
+     * stage barrier sits before the last k-step: by then every wave holds
+     * all fragments of the current stage in registers, so the last 16 MFMAs
+     * overlap the first fragment reads of the next stage. */
     const uint32_t k_steps = g.k / HK_BK;
-    load_global(0);
-    store_lds(0);
-    __syncthreads();
-
     const uint32_t frag_row = lane & 31u;
     const uint32_t frag_half = lane >> 5;
+    const uint32_t lds_base =
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)
+            hk_smem;
+    /* fragment rows are wn*128 + t*32 + frag_row (W) and wm*128 + t*32 +
+     * frag_row (X); their swizzle key only depends on frag_row & 15 */
+    const uint32_t w_row_base =
+        lds_base + HK_TILE_BYTES + (wn * 128u + frag_row) * 128u;
+    const uint32_t x_row_base = lds_base + (wm * 128u + frag_row) * 128u;
+    uint32_t chunk_off[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++)
+        chunk_off[ks] = ((ks * 2u + frag_half) ^ hk_swz_key(frag_row)) << 4;
+
+    hk_v4i fw[2][4], fx[2][4];
+    auto read_frags = [&](int buf, uint32_t stage, int ks) {
+        const uint32_t so = stage * HK_STAGE_BYTES + chunk_off[ks];
+        const uint32_t wa = w_row_base + so, xa = x_row_base + so;
+        asm volatile(
+            "ds_read_b128 %0, %8\n\t"
+            "ds_read_b128 %1, %8 offset:4096\n\t"
+            "ds_read_b128 %2, %8 offset:8192\n\t"
+            "ds_read_b128 %3, %8 offset:12288\n\t"
+            "ds_read_b128 %4, %9\n\t"
+            "ds_read_b128 %5, %9 offset:4096\n\t"
+            "ds_read_b128 %6, %9 offset:8192\n\t"
+            "ds_read_b128 %7, %9 offset:12288"
+            : "=&v"(fw[buf][0]), "=&v"(fw[buf][1]), "=&v"(fw[buf][2]),
+              "=&v"(fw[buf][3]), "=&v"(fx[buf][0]), "=&v"(fx[buf][1]),
+              "=&v"(fx[buf][2]), "=&v"(fx[buf][3])
+            : "v"(wa), "v"(xa));
+    };
+    auto wait_frags = [&](int buf) {
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(fw[buf][0]), "+v"(fw[buf][1]), "+v"(fw[buf][2]),
+                       "+v"(fw[buf][3]), "+v"(fx[buf][0]), "+v"(fx[buf][1]),
+                       "+v"(fx[buf][2]), "+v"(fx[buf][3]));
+    };
+    auto mfmas = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    __builtin_bit_cast(hk_bf16x8, fw[buf][i]),
+                    __builtin_bit_cast(hk_bf16x8, fx[buf][j]), acc[i][j], 0,
+                    0, 0);
+    };
+
+    issue_loads(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    read_frags(0, 0, 0);
+    wait_frags(0);
+#define HK_PIN() __builtin_amdgcn_sched_barrier(0)
     for (uint32_t kt = 0; kt < k_steps; kt++) {
         const uint32_t stage = kt & 1u;
-        if (kt + 1 < k_steps) load_global((kt + 1) * HK_BK);
-        const uint8_t *sx = hk_smem + stage * (2 * HK_TILE_BYTES);
-        const uint8_t *sw = sx + HK_TILE_BYTES;
-#pragma unroll
-        for (uint32_t ks = 0; ks < HK_BK / 16; ks++) {
-            const uint32_t chunk = ks * 2u + frag_half;
-            hk_bf16x8 wf[4], xf[4];
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const uint32_t wrow = wn * 128u + t * 32u + frag_row;
-                const uint32_t xrow = wm * 128u + t * 32u + frag_row;
-                wf[t] = *(const hk_bf16x8 *)(sw + hk_swz(wrow, chunk));
-                xf[t] = *(const hk_bf16x8 *)(sx + hk_swz(xrow, chunk));
-            }
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                        wf[i], xf[j], acc[i][j], 0, 0, 0);
-        }
-        if (kt + 1 < k_steps) store_lds(stage ^ 1u);
+        const bool more = kt + 1 < k_steps;
+        if (more) issue_loads(stage ^ 1u, (kt + 1) * HK_BK);
+        read_frags(1, stage, 1);
+        HK_PIN();
+        mfmas(0);
+        HK_PIN();
+        wait_frags(1);
+        read_frags(0, stage, 2);
+        HK_PIN();
+        mfmas(1);
+        HK_PIN();
+        wait_frags(0);
+        read_frags(1, stage, 3);
+        HK_PIN();
+        mfmas(0);
+        HK_PIN();
+        wait_frags(1);
+        /* every wave now holds the whole stage in registers; the next stage
+         * is complete once every wave's DMA has landed */
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
+        if (more) read_frags(0, stage ^ 1u, 0);
+        HK_PIN();
+        mfmas(1);
+        HK_PIN();
+        if (more) wait_frags(0);
     }
+#undef HK_PIN
 
     /* ---- epilogue ----
      * acc[i][j][r] = C[m][n] with

@@ -1,0 +1,418 @@
+"""Pins for the CPU oracle (oracle/h3_oracle.c) before it is trusted as the
+checker of the HIP backend.
+
+The reference's GPU arithmetic cannot run here (CUDA/Metal only), so each
+oracle function is pinned by checks chosen so that a plausible mistake -- a
+dropped term, a wrong slot or index, a transposed operand, a missing
+rounding -- fails one of them:
+  * exact small cases whose f32 arithmetic has no rounding at all;
+  * float64 restatements of the reference formulas (cited per test) with a
+    bound of one bf16 rounding;
+  * invariants: zero gate -> residual, scale = -1 & shift = 0 -> zero,
+    RoPE at position 0 -> identity and norm preservation, constant keys ->
+    mean of V, a dominant key -> its value row, SwiGLU of zero -> zero;
+  * the reference's own tiny op tests' shapes (tests/test_cuda_dit.c:135-143
+    ROW_MAP {2,0,3,1}, tests/test_cuda_core.c MLP 4x8x6x5).
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import bf16_ulp_distance, to_f32
+
+rng = np.random.default_rng(1234)
+
+
+def b(x):
+    return oracle.bf16(np.asarray(x, np.float32))
+
+
+def f64(bits):
+    return to_f32(bits).astype(np.float64)
+
+
+def within_one_rounding(got_bits, exact, extra=0.0):
+    """|got - exact| <= half a bf16 ulp of |exact| (+ extra)."""
+    g = f64(got_bits)
+    ex = np.asarray(exact, np.float64)
+    mag = np.maximum(np.abs(ex), 1e-30)
+    half_ulp = np.ldexp(1.0, np.frexp(mag)[1] - 9)
+    return np.all(np.abs(g - ex) <= half_ulp * 1.0001 + extra)
+
+
+# ---------------------------------------------------------------- linear
+
+def test_linear_exact_small_integers():
+    """Integer inputs: every partial sum is exact in f32, so the oracle must
+    equal the integer matrix product (checks operand order W[n,k] and the
+    bias)."""
+    m, k, n = 3, 5, 4
+    x = rng.integers(-4, 5, (m, k)).astype(np.float32)
+    w = rng.integers(-4, 5, (n, k)).astype(np.float32)
+    bias = rng.integers(-3, 4, n).astype(np.float32)
+    got = to_f32(oracle.linear(b(x), b(w), b(bias), m, k, n)).reshape(m, n)
+    np.testing.assert_array_equal(got, x @ w.T + bias)
+
+
+def test_linear_against_float64():
+    m, k, n = 37, 300, 70
+    x, w = b(rng.standard_normal(m * k)), b(0.1 * rng.standard_normal(n * k))
+    exact = f64(x).reshape(m, k) @ f64(w).reshape(n, k).T
+    got = oracle.linear(x, w, None, m, k, n)
+    # f32 sequential accumulation error bound k * 2^-24 * sum|x||w|
+    bound = k * 2.0 ** -24 * (np.abs(f64(x).reshape(m, k)) @
+                              np.abs(f64(w).reshape(n, k)).T)
+    assert within_one_rounding(got, exact.ravel(), bound.ravel())
+
+
+# ------------------------------------------------------------ row ops
+
+def _adaln64(x, w, mod, rm, rows, width, slots, shift, scale, eps):
+    x = f64(x).reshape(rows, width)
+    inv = 1.0 / np.sqrt((x * x).mean(axis=1, keepdims=True) + eps)
+    m = f64(mod).reshape(-1, slots, width)[np.asarray(rm)]
+    return (x * inv * f64(w)[None] * (1 + m[:, scale]) + m[:, shift]).ravel()
+
+
+def test_adaln_reference_shape_and_formula():
+    """tests/test_cuda_dit.c:135-143 shape: 4 rows, width 8, 3 slots,
+    ROW_MAP {2, 0, 3, 1}; h3_cuda_dit.cu:141-175 formula."""
+    rows, width, slots = 4, 8, 3
+    rm = np.array([2, 0, 3, 1], np.uint32)
+    x = b(rng.standard_normal(rows * width))
+    w = b(1 + 0.1 * rng.standard_normal(width))
+    mod = b(0.5 * rng.standard_normal(4 * slots * width))
+    got = oracle.adaln(x, w, mod, rm, rows, width, slots, 0, 1, 1e-5)
+    exact = _adaln64(x, w, mod, rm, rows, width, slots, 0, 1, 1e-5)
+    assert within_one_rounding(got, exact, 1e-6 * np.abs(exact) + 1e-7)
+    # slot order matters: swapping shift and scale must change the result
+    swapped = oracle.adaln(x, w, mod, rm, rows, width, slots, 1, 0, 1e-5)
+    assert not np.array_equal(swapped, got)
+
+
+def test_adaln_scale_minus_one_is_zero():
+    rows, width = 3, 64
+    x = b(rng.standard_normal(rows * width))
+    mod = np.zeros(2 * width, np.float32)
+    mod[width:] = -1.0                      # slot 1 = scale = -1, shift = 0
+    got = oracle.adaln(x, b(np.ones(width)), b(mod), [0, 0, 0], rows, width,
+                       2, 0, 1, 1e-5)
+    assert np.all(f64(got) == 0.0)
+
+
+def test_adaln_unit_rms():
+    rows, width = 5, 512
+    x = b(3 * rng.standard_normal(rows * width))
+    got = f64(oracle.adaln(x, b(np.ones(width)), b(np.zeros(2 * width)),
+                           [0] * rows, rows, width, 2, 0, 1, 0.0))
+    rms = np.sqrt((got.reshape(rows, width) ** 2).mean(axis=1))
+    np.testing.assert_allclose(rms, 1.0, atol=3e-3)
+
+
+def test_gate_bit_exact_and_zero_gate():
+    """h3_cuda_dit.cu:261-276: bf16(res + br * g).  bf16 x bf16 products and
+    their sum with a bf16 are exact in float64, so rounding the float64
+    value to f32 and then to bf16 is the same single rounding."""
+    rows, width, slots = 4, 16, 6
+    res, br = b(rng.standard_normal(rows * width)), b(
+        rng.standard_normal(rows * width))
+    mod = b(rng.standard_normal(3 * slots * width))
+    rm = np.array([2, 0, 1, 2], np.uint32)
+    got = oracle.gate(res, br, mod, rm, rows, width, slots, 4)
+    g = f64(mod).reshape(3, slots, width)[rm][:, 4]
+    exact = (f64(res).reshape(rows, width) + f64(br).reshape(rows, width) * g)
+    np.testing.assert_array_equal(got, b(exact.astype(np.float32).ravel()))
+    zero = oracle.gate(res, br, b(np.zeros(3 * slots * width)), rm, rows,
+                       width, slots, 4)
+    np.testing.assert_array_equal(zero, res)
+
+
+def test_gate_adaln_is_gate_then_adaln():
+    rows, width, slots = 6, 40, 6
+    res, br = b(rng.standard_normal(rows * width)), b(
+        rng.standard_normal(rows * width))
+    w = b(1 + 0.1 * rng.standard_normal(width))
+    gmod, nmod = b(rng.standard_normal(2 * slots * width)), b(
+        rng.standard_normal(2 * slots * width))
+    rm = np.array([1, 0, 1, 1, 0, 0], np.uint32)
+    gated, out = oracle.gate_adaln(res, br, w, gmod, nmod, rm, rows, width,
+                                   slots, 5, 0, 1, 1e-5)
+    np.testing.assert_array_equal(
+        gated, oracle.gate(res, br, gmod, rm, rows, width, slots, 5))
+    np.testing.assert_array_equal(
+        out, oracle.adaln(gated, w, nmod, rm, rows, width, slots, 0, 1, 1e-5))
+
+
+def test_layer_adaln_statistics_and_formula():
+    rows, width = 4, 256
+    x = b(2 + 3 * rng.standard_normal(rows * width))
+    plain = f64(oracle.layer_adaln(x, None, None, None, None, rows, width, 6,
+                                   0, 0, 0.0)).reshape(rows, width)
+    np.testing.assert_allclose(plain.mean(axis=1), 0, atol=3e-3)
+    np.testing.assert_allclose(plain.var(axis=1), 1, atol=6e-3)
+    w, bias = b(1 + 0.2 * rng.standard_normal(width)), b(
+        0.3 * rng.standard_normal(width))
+    mod = b(0.5 * rng.standard_normal(6 * width))
+    got = oracle.layer_adaln(x, w, bias, mod, [0] * rows, rows, width, 6, 3,
+                             4, 1e-6)
+    xf = f64(x).reshape(rows, width)
+    n = (xf - xf.mean(1, keepdims=True)) / np.sqrt(xf.var(1, keepdims=True) +
+                                                    1e-6)
+    m = f64(mod).reshape(6, width)
+    exact = ((n * f64(w) + f64(bias)) * (1 + m[4]) + m[3]).ravel()
+    assert within_one_rounding(got, exact, 1e-5 * (np.abs(n) + 1).ravel())
+
+
+def test_head_rms_norm():
+    rows, heads, hd = 3, 2, 128
+    t = b(rng.standard_normal(rows * heads * hd))
+    w = b(1 + 0.1 * rng.standard_normal(hd))
+    got = oracle.head_rms_norm(t, w, rows, heads, hd, 1e-6)
+    x = f64(t).reshape(rows * heads, hd)
+    exact = x / np.sqrt((x * x).mean(1, keepdims=True) + 1e-6) * f64(w)
+    assert within_one_rounding(got, exact.ravel(), 1e-6 * np.abs(exact).ravel())
+
+
+# ---------------------------------------------------------------- RoPE
+
+def _qkv_rope64(qkv, qw, kw, cos, sin, seq, heads, hd, half, grouped, eps):
+    x = f64(qkv).reshape(seq, -1)
+    out = []
+    for part, wt in ((0, qw), (1, kw)):
+        o = np.zeros((seq, heads, hd))
+        for h in range(heads):
+            if grouped:
+                v = x[:, h * 3 * hd + part * hd: h * 3 * hd + (part + 1) * hd]
+            else:
+                v = x[:, part * heads * hd + h * hd: part * heads * hd +
+                      (h + 1) * hd]
+            n = v / np.sqrt((v * v).mean(1, keepdims=True) + eps) * f64(wt)
+            c = f64(cos).reshape(seq, half)
+            s = f64(sin).reshape(seq, half)
+            r = n.copy()
+            r[:, :half] = n[:, :half] * c - n[:, half:2 * half] * s
+            r[:, half:2 * half] = n[:, half:2 * half] * c + n[:, :half] * s
+            o[:, h] = r
+        out.append(o.ravel())
+    return out
+
+
+@pytest.mark.parametrize("grouped", [True, False])
+def test_qkv_rope_formula(grouped):
+    """h3_cuda_attention.cu:175-237: per-head RMS, weight, rotate-half RoPE
+    on dims [0, 2*half); grouped rows [head][q,k,v][dim]."""
+    seq, heads, hd, half = 5, 2, 128, 48
+    qkv = b(rng.standard_normal(seq * 3 * heads * hd))
+    qw, kw = b(1 + 0.1 * rng.standard_normal(hd)), b(
+        1 + 0.1 * rng.standard_normal(hd))
+    ang = rng.uniform(-9, 9, seq * half)
+    cos, sin = b(np.cos(ang)), b(np.sin(ang))
+    q, k, v = oracle.qkv_rope(qkv, qw, kw, cos, sin, seq, heads, hd, half,
+                              grouped, 1e-5)
+    eq, ek = _qkv_rope64(qkv, qw, kw, cos, sin, seq, heads, hd, half, grouped,
+                         1e-5)
+    assert within_one_rounding(q, eq, 1e-5 * (np.abs(eq) + 0.05))
+    assert within_one_rounding(k, ek, 1e-5 * (np.abs(ek) + 0.05))
+    x = qkv.reshape(seq, -1)
+    vref = np.concatenate(
+        [x[:, h * 3 * hd + 2 * hd: h * 3 * hd + 3 * hd] if grouped
+         else x[:, 2 * heads * hd + h * hd: 2 * heads * hd + (h + 1) * hd]
+         for h in range(heads)], axis=1)
+    np.testing.assert_array_equal(v, vref.ravel())
+
+
+def test_rope_identity_and_norm_preservation():
+    seq, heads, hd, half = 4, 1, 128, 48
+    qkv = b(rng.standard_normal(seq * 3 * hd))
+    ones = b(np.ones(hd))
+    q0, _, _ = oracle.qkv_rope(qkv, ones, ones, b(np.ones(seq * half)),
+                               b(np.zeros(seq * half)), seq, heads, hd, half,
+                               True, 0.0)
+    qn, _, _ = oracle.qkv_rope(qkv, ones, ones, b(np.ones(seq * half)),
+                               b(np.zeros(seq * half)), seq, heads, hd, 0,
+                               True, 0.0)
+    np.testing.assert_array_equal(q0, qn)       # angle 0 == no rotation
+    ang = rng.uniform(-5, 5, seq * half)
+    c, s = np.cos(ang), np.sin(ang)
+    qr, _, _ = oracle.qkv_rope(qkv, ones, ones, b(c), b(s), seq, heads, hd,
+                               half, True, 0.0)
+    n0 = (f64(q0).reshape(seq, hd) ** 2).sum(1)
+    n1 = (f64(qr).reshape(seq, hd) ** 2).sum(1)
+    np.testing.assert_allclose(n1, n0, rtol=2e-2)   # rotation keeps norm
+
+
+# ------------------------------------------------------------ attention
+
+def _sdpa64(q, k, v, nq, nk, heads, hd, scale):
+    qf = f64(q).reshape(nq, heads, hd)
+    kf = f64(k).reshape(nk, heads, hd)
+    vf = f64(v).reshape(nk, heads, hd)
+    s = np.einsum("qhd,khd->hqk", qf, kf) * scale
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    return np.einsum("hqk,khd->qhd", p, vf).ravel()
+
+
+@pytest.mark.parametrize("round_p", [False, True])
+def test_sdpa_against_float64(round_p):
+    nq, nk, heads, hd = 9, 33, 2, 128
+    q, k, v = (b(rng.standard_normal(n * heads * hd)) for n in (nq, nk, nk))
+    scale = 1 / math.sqrt(hd)
+    got = f64(oracle.sdpa(q, k, v, nq, nk, heads, hd, scale,
+                          round_p=round_p))
+    exact = _sdpa64(q, k, v, nq, nk, heads, hd, scale)
+    tol = 1e-3 + (1e-2 if round_p else 4e-3) * np.abs(exact)
+    assert np.all(np.abs(got - exact) <= tol)
+
+
+def test_sdpa_invariants():
+    nq, nk, hd = 3, 50, 128
+    q = b(rng.standard_normal(nq * hd))
+    v = b(rng.standard_normal(nk * hd))
+    k = np.tile(b(rng.standard_normal(hd)), nk)
+    got = f64(oracle.sdpa(q, k, v, nq, nk, 1, hd, 0.1)).reshape(nq, hd)
+    np.testing.assert_allclose(got, np.tile(f64(v).reshape(nk, hd).mean(0),
+                                            (nq, 1)), atol=2e-2)
+    # one key aligned with the query dominates: output = that value row
+    kk = b(np.zeros(nk * hd)).reshape(nk, hd)
+    kk[17] = b(np.full(hd, 4.0))
+    qq = b(np.full(nq * hd, 4.0))
+    got = oracle.sdpa(qq, kk.ravel(), v, nq, nk, 1, hd, 1.0).reshape(nq, hd)
+    np.testing.assert_array_equal(got, np.tile(v.reshape(nk, hd)[17],
+                                               (nq, 1)))
+    hm = oracle.sdpa(q, k, v, nq, nk, 1, hd, 0.1, head_major=True)
+    rm = oracle.sdpa(q, k, v, nq, nk, 1, hd, 0.1)
+    np.testing.assert_array_equal(hm, rm)  # one head: both layouts coincide
+
+
+# -------------------------------------------------- elementwise and MLP
+
+def test_swiglu_gelu_silu_formulas():
+    rows, width = 3, 100
+    fused = b(3 * rng.standard_normal(rows * 2 * width))
+    got = oracle.swiglu(fused, rows, width)
+    fz = f64(fused).reshape(rows, 2 * width)
+    g, u = fz[:, :width], fz[:, width:]
+    exact = (g / (1 + np.exp(-g)) * u).ravel()
+    assert within_one_rounding(got, exact, 1e-6 * np.abs(exact))
+    assert np.all(f64(oracle.swiglu(b(np.zeros(2 * width)), 1, width)) == 0)
+    x = b(np.linspace(-12, 12, 301))
+    xf = f64(x)
+    inner = 0.7978845608028654 * (xf + 0.044715 * xf ** 3)
+    exact = np.where(inner <= -10, 0.0, np.where(inner >= 10, xf,
+                     0.5 * xf * (1 + np.tanh(inner))))
+    # the reference's f32 formula loses |x| * 2^-23 or so to the cancellation
+    # in 1 + tanh(inner) for large negative x; allow that f32 error
+    assert within_one_rounding(oracle.gelu(x), exact,
+                               1e-6 * np.abs(exact) + np.abs(xf) * 2.0 ** -22)
+    # a wrong cubic coefficient or the erf form would not pass:
+    wrong = 0.5 * xf * (1 + np.tanh(0.7978845608028654 * (xf + 0.05 * xf ** 3)))
+    assert not within_one_rounding(oracle.gelu(x), wrong,
+                                   np.abs(xf) * 2.0 ** -22)
+    assert within_one_rounding(oracle.silu(x), xf / (1 + np.exp(-xf)),
+                               1e-6 * np.abs(xf))
+
+
+def test_mlp_reference_tiny_shape():
+    """tests/test_cuda_core.c:1071-1110 shape (rows 4, in 8, hidden 6,
+    out 5): fc1 rows [0, hidden) are the gate, [hidden, 2 hidden) the up
+    projection."""
+    rows, d, hid, out = 4, 8, 6, 5
+    x, fc1, fc2 = (b(s * rng.standard_normal(n)) for s, n in
+                   ((1.0, rows * d), (0.5, 2 * hid * d), (0.5, out * hid)))
+    got = oracle.linear(oracle.swiglu(oracle.linear(x, fc1, None, rows, d,
+                                                    2 * hid), rows, hid),
+                        fc2, None, rows, hid, out)
+    # float64 restatement with the two bf16 boundaries of the GEMM path
+    fz = f64(x).reshape(rows, d) @ f64(fc1).reshape(2 * hid, d).T
+    fz = f64(b(fz.astype(np.float32)))
+    g, u = fz[:, :hid], fz[:, hid:]
+    act = f64(b((g / (1 + np.exp(-g)) * u).astype(np.float32)))
+    exact = act @ f64(fc2).reshape(out, hid).T
+    # a one-ulp flip of an intermediate (g, u or the activation) may
+    # propagate: allow 4 bf16 ulps of the activations through fc2
+    bound = np.abs(act) @ np.abs(f64(fc2).reshape(out, hid)).T * 2.0 ** -6
+    assert within_one_rounding(got, exact.ravel(), bound.ravel())
+    # gate and up swapped must not pass
+    swapped = (u / (1 + np.exp(-u)) * g) @ f64(fc2).reshape(out, hid).T
+    assert not within_one_rounding(got, swapped.ravel(), bound.ravel())
+
+
+def test_euler_closed_form():
+    """h3_cuda_dit.cu:536-548: x + delta (v + r (v - v_prev))."""
+    s = rng.standard_normal(64).astype(np.float32)
+    last, prev = b(rng.standard_normal(64)), b(rng.standard_normal(64))
+    got = oracle.euler(s, last, prev, 0.125, -0.5)
+    exact = s + 0.125 * (f64(last) - 0.5 * (f64(last) - f64(prev)))
+    np.testing.assert_allclose(got, exact, rtol=2e-7, atol=1e-7)
+    np.testing.assert_array_equal(oracle.euler(s, last, prev, 0.0, 1.0), s)
+
+
+def test_final_head_formula():
+    rows, width, n = 3, 64, 5
+    x = b(rng.standard_normal(rows * width))
+    nw = b(1 + 0.1 * rng.standard_normal(width))
+    mod = b(0.3 * rng.standard_normal(2 * 2 * width))
+    w, bias = b(0.2 * rng.standard_normal(n * width)), b(rng.standard_normal(n))
+    rm = np.array([1, 0, 1], np.uint32)
+    got, inv = oracle.adaln_linear(x, nw, mod, rm, w, bias, rows, width, n, 2,
+                                   0, 1, 1e-5)
+    normed = oracle.adaln(x, nw, mod, rm, rows, width, 2, 0, 1, 1e-5)
+    np.testing.assert_array_equal(got, oracle.linear(normed, w, bias, rows,
+                                                     width, n))
+    xf = f64(x).reshape(rows, width)
+    np.testing.assert_allclose(inv, 1 / np.sqrt((xf * xf).mean(1) + 1e-5),
+                               rtol=1e-6)
+
+
+def test_patch_linear_exact_and_mapped():
+    rows, k, n = 4, 6, 5
+    x = rng.integers(-3, 4, (rows, k)).astype(np.float32)
+    w = rng.integers(-3, 4, (n, k)).astype(np.float32)
+    bias = rng.integers(-2, 3, n).astype(np.float32)
+    rm = np.array([3, 0, 5, 1], np.uint32)
+    got = to_f32(oracle.patch_linear(x, w, bias, rows, k, n, row_map=rm,
+                                     out_rows=6)).reshape(6, n)
+    want = np.zeros((6, n), np.float32)
+    want[rm] = x @ w.T + bias
+    np.testing.assert_array_equal(got, want)
+
+
+# ---------------------------------------------------- block composition
+
+def test_h3_blocks_zero_gates_leave_residual():
+    """With gate slots 2 and 5 at zero both residual updates vanish, so any
+    number of H3 blocks returns the input bit for bit (h3_dit.c:2100-2177
+    order: attention gate, MLP gate, fused next-block adaLN)."""
+    rows, d, heads, ffn = 20, 256, 2, 256
+    hd = 128
+    x = b(rng.standard_normal(rows * d))
+
+    def block():
+        mod = 0.3 * rng.standard_normal((1, 3, 6, d))
+        mod[:, :, 2] = 0
+        mod[:, :, 5] = 0
+        return {"norm1": b(np.ones(d)), "norm2": b(np.ones(d)),
+                "qkv": b(0.05 * rng.standard_normal(3 * heads * hd * d)),
+                "q_norm": b(np.ones(hd)), "k_norm": b(np.ones(hd)),
+                "out": b(0.05 * rng.standard_normal(d * heads * hd)),
+                "fc1": b(0.05 * rng.standard_normal(2 * ffn * d)),
+                "fc2": b(0.05 * rng.standard_normal(d * ffn)),
+                "modulation": b(mod.ravel())}
+    ang = rng.uniform(-3, 3, rows * 48)
+    out = oracle.h3_blocks(x, [block(), block()], np.zeros(rows, np.uint32),
+                           b(np.cos(ang)), b(np.sin(ang)), rows, d, heads,
+                           ffn)
+    np.testing.assert_array_equal(out, x)
+
+
+def test_bf16_rounding_is_rne():
+    """RNE ties: 1 + 2^-8 is halfway between 1 and 1 + 2^-7 -> even (1);
+    1 + 3 * 2^-8 -> 1 + 2^-6 (even mantissa)."""
+    vals = np.array([1 + 2 ** -8, 1 + 3 * 2 ** -8, -(1 + 2 ** -8), 1e-40,
+                     65504.0], np.float32)
+    got = to_f32(b(vals))
+    assert got[0] == 1.0 and got[1] == 1 + 2 ** -6 and got[2] == -1.0
+    assert bf16_ulp_distance(b(vals[3:4]), b(np.float32(1e-40))) == 0
