@@ -99,23 +99,63 @@ def time_forward(gpu, dit, blocks, steps, warmup):
     return ms.value / steps, wall * 1000.0 / steps
 
 
-def op_profile(gpu, dit, blocks):
-    """One forward with per-op HIP-event timing; {op: (count, ms)}."""
+OPS_GEMM, OPS_ACT, OPS_ATTN, OPS_ROWS = 1, 2, 4, 8
+
+
+def class_replay(gpu, dit, blocks, mask, reps=2):
+    """Device ms of one forward's launches of one op class: the driver
+    re-issues exactly those launches (same shapes, same tensors) for all
+    blocks, bracketed by two HIP events on the backend's stream."""
     import ctypes as C
     L = gpu.L
-    L.h3_hip_op_timing_enable(gpu.h, 1)
-    L.h3_hip_op_timing_reset(gpu.h)
+    gpu.begin()
+    if not L.h3hip_dit_run_blocks_ops(dit.h, 0, blocks, mask):  # warm
+        raise RuntimeError(dit.error())
+    L.h3_hip_marker(gpu.h, 2)
+    for _ in range(reps):
+        if not L.h3hip_dit_run_blocks_ops(dit.h, 0, blocks, mask):
+            raise RuntimeError(dit.error())
+    L.h3_hip_marker(gpu.h, 3)
+    gpu.submit()
+    ms = C.c_double()
+    L.h3_hip_marker_elapsed(gpu.h, 2, 3, C.byref(ms))
+    return ms.value / reps
+
+
+def profile_pass(gpu, dit, blocks):
+    """Launch pattern for counter collection: warm-up forward, one forward,
+    one replay of the plain GEMMs, then add_bf16 over 64 Mi elements (reads
+    2 x 128 MiB, writes 128 MiB) whose FETCH_SIZE / WRITE_SIZE readings scale
+    the GEMM's counters to bytes."""
     dit.run_blocks(0, blocks)
-    names = C.create_string_buffer(4096)
-    L.h3_hip_op_timing_names(gpu.h, names, 4096)
-    out = {}
-    for name in names.value.decode().split():
-        n, ms = C.c_uint64(), C.c_double()
-        L.h3_hip_op_timing_read(gpu.h, name.encode(), C.byref(n), C.byref(ms))
-        out[name] = (n.value, ms.value)
-    L.h3_hip_op_timing_enable(gpu.h, 0)
-    L.h3_hip_op_timing_reset(gpu.h)
-    return out
+    dit.run_blocks(0, blocks)
+    L = gpu.L
+    gpu.begin()
+    if not L.h3hip_dit_run_blocks_ops(dit.h, 0, blocks, OPS_GEMM):
+        raise RuntimeError(dit.error())
+    gpu.submit()
+    n = 64 << 20
+    a, b, c = gpu.new_bf16(n), gpu.new_bf16(n), gpu.new_bf16(n)
+    gpu.begin()
+    L.h3_gpu_fill_normal_bf16(gpu.h, a, 0, n, 5, 0.0, 1.0)
+    L.h3_gpu_fill_normal_bf16(gpu.h, b, 0, n, 6, 0.0, 1.0)
+    gpu.check(L.h3_gpu_add_bf16(gpu.h, c, a, b, n), "calibration add")
+    gpu.submit()
+    log("profile pass done")
+
+
+def load_traffic(name):
+    """HBM bytes per launch of the dominant kernel, measured offline with two
+    rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) and calibrated on a copy
+    kernel; see profiles/.  None when no measurement is on file."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    try:
+        with open(path) as f:
+            return json.load(f).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
 
 
 def cpu_baseline(seconds_budget=30.0):
@@ -169,6 +209,11 @@ def main():
     ap.add_argument("--blocks", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-h3", action="store_true")
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="for rocprofv3 runs: one forward, one replay of the "
+                         "plain GEMMs, one 64 Mi-element copy-like kernel of "
+                         "known traffic (add_bf16) as the counter "
+                         "calibration; no timing line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this backend runs on one GPU; the "
@@ -194,16 +239,29 @@ def main():
         __import__("ctypes").byref(cfg))
     attn_flops = gpu.L.h3hip_dit_block_attention_flops(
         __import__("ctypes").byref(cfg))
+    if args.profile_pass:
+        profile_pass(gpu, dit, blocks)
+        dit.close()
+        gpu.close()
+        return
     log("timing ...")
     ms_step, wall_ms = time_forward(gpu, dit, blocks, args.steps, args.warmup)
-    prof = op_profile(gpu, dit, blocks)
     total_tflops = blocks * block_flops / (ms_step / 1e3) / 1e12
-    gemm_n = sum(v[0] for k, v in prof.items() if k.startswith("gemm"))
-    gemm_ms = sum(v[1] for k, v in prof.items() if k.startswith("gemm"))
-    attn_ms = sum(v[1] for k, v in prof.items() if k.startswith("attention"))
-    attn_n = sum(v[0] for k, v in prof.items() if k.startswith("attention"))
-    gemm_tflops = blocks * gemm_flops / (gemm_ms / 1e3) / 1e12
+    log("per-class replays ...")
+    L = gpu.L
+    cref = __import__("ctypes").byref(cfg)
+    plain_flops = L.h3hip_dit_block_plain_gemm_flops(cref)
+    plain_launches = L.h3hip_dit_block_plain_gemm_launches(cref)
+    gemm_ms = class_replay(gpu, dit, blocks, OPS_GEMM)
+    act_ms = class_replay(gpu, dit, blocks, OPS_ACT)
+    attn_ms = class_replay(gpu, dit, blocks, OPS_ATTN)
+    rows_ms = class_replay(gpu, dit, blocks, OPS_ROWS)
+    act_flops = gemm_flops - plain_flops
+    gemm_tflops = blocks * plain_flops / (gemm_ms / 1e3) / 1e12
+    act_tflops = blocks * act_flops / (act_ms / 1e3) / 1e12
     attn_tflops = blocks * attn_flops / (attn_ms / 1e3) / 1e12
+    per_launch_flops = plain_flops / plain_launches
+    per_launch_ms = gemm_ms / (blocks * plain_launches)
     dit.close()
 
     h3_real = None
@@ -253,19 +311,36 @@ def main():
         "mfma_util_pct": round(100 * total_tflops / BF16_PEAK_TFLOPS, 1),
         "wall_ms_per_step": round(wall_ms, 3),
         "kernels": {
-            "gemm": {"tflops": round(gemm_tflops, 1),
-                     "frac_of_peak": round(gemm_tflops / BF16_PEAK_TFLOPS, 4),
-                     "launches": gemm_n, "ms": round(gemm_ms, 3)},
-            "attention": {"tflops": round(attn_tflops, 1),
+            "gemm_plain": {"kernel": "hk_gemm_mfma<0>",
+                           "tflops": round(gemm_tflops, 1),
+                           "frac_of_peak": round(gemm_tflops /
+                                                 BF16_PEAK_TFLOPS, 4),
+                           "launches_per_forward": blocks * plain_launches,
+                           "avg_launch_us": round(per_launch_ms * 1e3, 1),
+                           "ms_per_forward": round(gemm_ms, 3)},
+            "gemm_gelu": {"kernel": "hk_gemm_mfma<2>",
+                          "tflops": round(act_tflops, 1),
+                          "frac_of_peak": round(act_tflops /
+                                                BF16_PEAK_TFLOPS, 4),
+                          "ms_per_forward": round(act_ms, 3)},
+            "attention": {"kernel": "hk_flash_fwd",
+                          "tflops": round(attn_tflops, 1),
                           "frac_of_peak": round(attn_tflops /
                                                 BF16_PEAK_TFLOPS, 4),
-                          "launches": attn_n, "ms": round(attn_ms, 3)},
-            "ops_ms": {k: round(v[1], 3) for k, v in sorted(prof.items())},
+                          "ms_per_forward": round(attn_ms, 3)},
+            "row_ops": {"ms_per_forward": round(rows_ms, 3)},
         },
-        "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 1),
+        "roofline": {"kernel": "hk_gemm_mfma<0> (plain-epilogue GEMMs of "
+                               "the forward)",
+                     "bound": "mfma",
+                     "achieved": round(per_launch_flops / (per_launch_ms /
+                                                           1e3) / 1e12, 1),
                      "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(gemm_tflops / BF16_PEAK_TFLOPS, 4),
-                     "traffic": None},
+                     "frac": round(per_launch_flops / (per_launch_ms / 1e3) /
+                                   1e12 / BF16_PEAK_TFLOPS, 4),
+                     "flops_per_launch": per_launch_flops,
+                     "avg_launch_us": round(per_launch_ms * 1e3, 1),
+                     "traffic": load_traffic("gemm_plain_wan512_traffic.json")},
         "h3_real_shape": h3_real,
         "cpu_baseline": base,
     }

@@ -166,6 +166,11 @@ def lib():
         "h3hip_dit_set_row_map": (_I, [_P, _P]),
         "h3hip_dit_tensor": (_P, [_P, C.c_char_p, _U32]),
         "h3hip_dit_run_blocks": (_I, [_P, _U32, _U32]),
+        "h3hip_dit_run_blocks_ops": (_I, [_P, _U32, _U32, C.c_uint]),
+        "h3hip_dit_block_plain_gemm_flops": (C.c_double,
+                                             [C.POINTER(DitConfig)]),
+        "h3hip_dit_block_plain_gemm_launches": (_U32,
+                                                [C.POINTER(DitConfig)]),
         "h3hip_dit_block_flops": (C.c_double, [C.POINTER(DitConfig)]),
         "h3hip_dit_block_gemm_flops": (C.c_double, [C.POINTER(DitConfig)]),
         "h3hip_dit_block_attention_flops": (C.c_double,
@@ -196,12 +201,22 @@ def lib():
         "h3hip_unpack_audio": (_I, [_P, _I, _I, _P, _SZ]),
         "h3hip_euler_velocity_step": (_I, [_P, _P, _SZ, _F, _F]),
     }
+    ns = _Prototyped()
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
         fn.restype = res
         fn.argtypes = args
-    _lib = L
-    return L
+        setattr(ns, name, fn)
+    _lib = ns
+    return ns
+
+
+class _Prototyped:
+    """Only functions with a declared prototype are reachable: calling an
+    undeclared one would let ctypes truncate 64-bit pointers to int."""
+
+    def __getattr__(self, name):
+        raise AttributeError(f"{name} has no ctypes prototype in h3hip.py")
 
 
 def ptr(a):

@@ -26,8 +26,9 @@ struct h3hip_dit {
     /* shared state and activations */
     h3_gpu_tensor *hidden, *row_map, *rope_cos, *rope_sin, *context;
     h3_gpu_tensor *mod_a, *mod_b, *qkv, *query, *key, *value, *attn, *proj;
-    h3_gpu_tensor *cross_q, *cross_k, *cross_v, *cross_out;
+    h3_gpu_tensor *cross_q, *cross_k, *cross_v, *cross_out, *ffn_act;
     int attention_adaln_ready;
+    unsigned op_mask;
     char error[512];
 };
 
@@ -43,6 +44,14 @@ static int dit_op(h3hip_dit *dit, int ok, const char *what) {
     if (ok) return 1;
     return dit_fail(dit, "%s: %s", what, h3_gpu_error(dit->gpu));
 }
+
+/* Issue `call` only when its op class is enabled (see run_blocks_ops). */
+#define DIT_OP(klass, call, what)                                           \
+    ((dit->op_mask & (klass)) ? dit_op(dit, (call), (what)) : 1)
+#define K_GEMM H3HIP_OPS_GEMM
+#define K_ACT H3HIP_OPS_GEMM_ACT
+#define K_ATTN H3HIP_OPS_ATTENTION
+#define K_ROWS H3HIP_OPS_ROWS
 
 const char *h3hip_dit_error(const h3hip_dit *dit) {
     return dit ? dit->error : "no DiT";
@@ -166,6 +175,7 @@ h3hip_dit *h3hip_dit_create(h3_gpu *gpu, const h3hip_dit_config *config,
         dit->cross_k = bf16(dit, t * inner, &ok);
         dit->cross_v = bf16(dit, t * inner, &ok);
         dit->cross_out = bf16(dit, n * inner, &ok);
+        dit->ffn_act = bf16(dit, n * f, &ok);
     }
     if (!ok) {
         if (error && error_size)
@@ -191,7 +201,7 @@ void h3hip_dit_free(h3hip_dit *dit) {
         dit->hidden, dit->row_map, dit->rope_cos, dit->rope_sin,
         dit->context, dit->mod_a, dit->mod_b, dit->qkv, dit->query,
         dit->key, dit->value, dit->attn, dit->proj, dit->cross_q,
-        dit->cross_k, dit->cross_v, dit->cross_out};
+        dit->cross_k, dit->cross_v, dit->cross_out, dit->ffn_act};
     for (size_t i = 0; i < sizeof(shared) / sizeof(*shared); i++)
         h3_gpu_tensor_free(shared[i]);
     free(dit);
@@ -340,37 +350,41 @@ static int run_h3_block(h3hip_dit *dit, uint32_t index, int fuse_next) {
     const float eps = c->epsilon;
     const uint32_t slots = SLOTS;
     if (!dit->attention_adaln_ready &&
-        !dit_op(dit, h3_gpu_adaln_bf16(gpu, dit->mod_a, dit->hidden,
+        !DIT_OP(K_ROWS, h3_gpu_adaln_bf16(gpu, dit->mod_a, dit->hidden,
                                        w->norm1, w->modulation, dit->row_map,
                                        rows, hidden, slots, 0, 1, eps),
                 "attention adaLN"))
         return 0;
     dit->attention_adaln_ready = 0;
-    if (!dit_op(dit, h3_gpu_grouped_qkv_linear_rope_bf16(
+    /* h3_gpu_grouped_qkv_linear_rope_bf16 is exactly these two calls on
+     * this backend; issuing them separately keeps the op classes apart */
+    if (!DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->qkv, dit->mod_a, w->qkv,
+                                        NULL, rows, hidden, 3 * inner),
+                "QKV projection") ||
+        !DIT_OP(K_ROWS, h3_gpu_grouped_qkv_rope_bf16(
                          gpu, dit->query, dit->key, dit->value, dit->qkv,
-                         dit->mod_a, w->qkv, w->q_norm, w->k_norm,
-                         dit->rope_cos, dit->rope_sin, rows, hidden, c->heads,
-                         c->head_dim, c->rope_half, eps),
-                "QKV projection/norm/RoPE") ||
-        !dit_op(dit, h3_gpu_sdpa_bf16(gpu, dit->attn, dit->query, dit->key,
+                         w->q_norm, w->k_norm, dit->rope_cos, dit->rope_sin,
+                         rows, c->heads, c->head_dim, c->rope_half, eps),
+                "Q/K norm + RoPE") ||
+        !DIT_OP(K_ATTN, h3_gpu_sdpa_bf16(gpu, dit->attn, dit->query, dit->key,
                                       dit->value, rows, c->heads, c->head_dim,
                                       1.0f / sqrtf((float)c->head_dim)),
                 "joint attention") ||
-        !dit_op(dit, h3_gpu_linear_bf16(gpu, dit->proj, dit->attn, w->out,
+        !DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->proj, dit->attn, w->out,
                                         NULL, rows, inner, hidden),
                 "attention output") ||
-        !dit_op(dit, h3_gpu_gate_adaln_bf16(
+        !DIT_OP(K_ROWS, h3_gpu_gate_adaln_bf16(
                          gpu, dit->hidden, dit->mod_b, dit->hidden, dit->proj,
                          w->norm2, w->modulation, w->modulation, dit->row_map,
                          rows, hidden, slots, 2, 3, 4, eps),
                 "attention gate + MLP adaLN") ||
-        !dit_op(dit, h3_gpu_mlp_bf16(gpu, dit->proj, dit->mod_b, w->fc1,
+        !DIT_OP(K_ACT, h3_gpu_mlp_bf16(gpu, dit->proj, dit->mod_b, w->fc1,
                                      w->fc2, rows, hidden, c->ffn, hidden),
                 "SwiGLU MLP"))
         return 0;
     if (fuse_next) {
         h3hip_block *next = &dit->blocks[index + 1];
-        if (!dit_op(dit, h3_gpu_gate_adaln_bf16(
+        if (!DIT_OP(K_ROWS, h3_gpu_gate_adaln_bf16(
                              gpu, dit->hidden, dit->mod_a, dit->hidden,
                              dit->proj, next->norm1, w->modulation,
                              next->modulation, dit->row_map, rows, hidden,
@@ -380,7 +394,7 @@ static int run_h3_block(h3hip_dit *dit, uint32_t index, int fuse_next) {
         dit->attention_adaln_ready = 1;
         return 1;
     }
-    return dit_op(dit, h3_gpu_gate_bf16(gpu, dit->hidden, dit->hidden,
+    return DIT_OP(K_ROWS, h3_gpu_gate_bf16(gpu, dit->hidden, dit->hidden,
                                         dit->proj, w->modulation, dit->row_map,
                                         rows, hidden, slots, 5),
                   "MLP gate");
@@ -395,80 +409,105 @@ static int run_wan_block(h3hip_dit *dit, uint32_t index) {
     const uint32_t inner = c->heads * c->head_dim;
     const float eps = c->epsilon;
     const float scale = 1.0f / sqrtf((float)c->head_dim);
-    return dit_op(dit, h3_gpu_layer_adaln_bf16(
+    return DIT_OP(K_ROWS, h3_gpu_layer_adaln_bf16(
                            gpu, dit->mod_a, dit->hidden, NULL, NULL,
                            w->modulation, dit->row_map, rows, d, SLOTS, 0, 1,
                            eps),
                   "self-attention adaLN") &&
-           dit_op(dit, h3_gpu_linear_bf16(gpu, dit->qkv, dit->mod_a, w->qkv,
+           DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->qkv, dit->mod_a, w->qkv,
                                           w->qkv_bias, rows, d, 3 * inner),
                   "QKV projection") &&
-           dit_op(dit, h3_gpu_qkv_rope_bf16(
+           DIT_OP(K_ROWS, h3_gpu_qkv_rope_bf16(
                            gpu, dit->query, dit->key, dit->value, dit->qkv,
                            w->q_norm, w->k_norm, dit->rope_cos, dit->rope_sin,
                            rows, c->heads, c->head_dim, c->rope_half, eps),
                   "Q/K norm + RoPE") &&
-           dit_op(dit, h3_gpu_sdpa_bf16(gpu, dit->attn, dit->query, dit->key,
+           DIT_OP(K_ATTN, h3_gpu_sdpa_bf16(gpu, dit->attn, dit->query, dit->key,
                                         dit->value, rows, c->heads,
                                         c->head_dim, scale),
                   "self-attention") &&
-           dit_op(dit, h3_gpu_linear_bf16(gpu, dit->proj, dit->attn, w->out,
+           DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->proj, dit->attn, w->out,
                                           w->out_bias, rows, inner, d),
                   "self-attention output") &&
-           dit_op(dit, h3_gpu_gate_bf16(gpu, dit->hidden, dit->hidden,
+           DIT_OP(K_ROWS, h3_gpu_gate_bf16(gpu, dit->hidden, dit->hidden,
                                         dit->proj, w->modulation,
                                         dit->row_map, rows, d, SLOTS, 2),
                   "self-attention gate") &&
-           dit_op(dit, h3_gpu_layer_adaln_bf16(
+           DIT_OP(K_ROWS, h3_gpu_layer_adaln_bf16(
                            gpu, dit->mod_b, dit->hidden, w->norm3,
                            w->norm3_bias, NULL, NULL, rows, d, SLOTS, 0, 0,
                            eps),
                   "cross-attention norm") &&
-           dit_op(dit, h3_gpu_linear_bf16(gpu, dit->cross_q, dit->mod_b,
+           DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->cross_q, dit->mod_b,
                                           w->cq, w->cq_bias, rows, d, inner),
                   "cross Q projection") &&
-           dit_op(dit, h3_gpu_head_rms_norm_bf16(gpu, dit->cross_q,
+           DIT_OP(K_ROWS, h3_gpu_head_rms_norm_bf16(gpu, dit->cross_q,
                                                  w->cq_norm, rows, c->heads,
                                                  c->head_dim, eps),
                   "cross Q norm") &&
-           dit_op(dit, h3_gpu_linear_bf16(gpu, dit->cross_k, dit->context,
+           DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->cross_k, dit->context,
                                           w->ck, w->ck_bias, t, d, inner),
                   "cross K projection") &&
-           dit_op(dit, h3_gpu_head_rms_norm_bf16(gpu, dit->cross_k,
+           DIT_OP(K_ROWS, h3_gpu_head_rms_norm_bf16(gpu, dit->cross_k,
                                                  w->ck_norm, t, c->heads,
                                                  c->head_dim, eps),
                   "cross K norm") &&
-           dit_op(dit, h3_gpu_linear_bf16(gpu, dit->cross_v, dit->context,
+           DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->cross_v, dit->context,
                                           w->cv, w->cv_bias, t, d, inner),
                   "cross V projection") &&
-           dit_op(dit, h3_gpu_sdpa_cross_bf16(gpu, dit->cross_out,
+           DIT_OP(K_ATTN, h3_gpu_sdpa_cross_bf16(gpu, dit->cross_out,
                                               dit->cross_q, dit->cross_k,
                                               dit->cross_v, rows, t, c->heads,
                                               c->head_dim, scale),
                   "cross-attention") &&
-           dit_op(dit, h3_gpu_linear_bf16(gpu, dit->proj, dit->cross_out,
+           DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->proj, dit->cross_out,
                                           w->co, w->co_bias, rows, inner, d),
                   "cross-attention output") &&
-           dit_op(dit, h3_gpu_add_bf16(gpu, dit->hidden, dit->hidden,
+           DIT_OP(K_ROWS, h3_gpu_add_bf16(gpu, dit->hidden, dit->hidden,
                                        dit->proj, rows * d),
                   "cross-attention residual") &&
-           dit_op(dit, h3_gpu_layer_adaln_bf16(
+           DIT_OP(K_ROWS, h3_gpu_layer_adaln_bf16(
                            gpu, dit->mod_a, dit->hidden, NULL, NULL,
                            w->modulation, dit->row_map, rows, d, SLOTS, 3, 4,
                            eps),
                   "FFN adaLN") &&
-           dit_op(dit, h3_gpu_ffn_gelu_bf16(gpu, dit->proj, NULL, dit->mod_a,
-                                            w->fc1, w->fc1_bias, w->fc2,
-                                            w->fc2_bias, rows, d, c->ffn, d),
-                  "GELU FFN") &&
-           dit_op(dit, h3_gpu_gate_bf16(gpu, dit->hidden, dit->hidden,
+           DIT_OP(K_ACT, h3_gpu_linear_gelu_bf16(gpu, dit->ffn_act,
+                                               dit->mod_a, w->fc1,
+                                               w->fc1_bias, rows, d, c->ffn),
+                  "FFN up + GELU") &&
+           DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->proj, dit->ffn_act,
+                                          w->fc2, w->fc2_bias, rows, c->ffn,
+                                          d),
+                  "FFN down") &&
+           DIT_OP(K_ROWS, h3_gpu_gate_bf16(gpu, dit->hidden, dit->hidden,
                                         dit->proj, w->modulation,
                                         dit->row_map, rows, d, SLOTS, 5),
                   "FFN gate");
 }
 
 int h3hip_dit_run_blocks(h3hip_dit *dit, uint32_t first, uint32_t count) {
+    return h3hip_dit_run_blocks_ops(dit, first, count, H3HIP_OPS_ALL);
+}
+
+double h3hip_dit_block_plain_gemm_flops(const h3hip_dit_config *c) {
+    double d = c->hidden, inner = (double)c->heads * c->head_dim;
+    double n = c->rows, f = c->ffn;
+    if (c->family == H3HIP_FAMILY_WAN)
+        /* qkv, out, cross q, cross out, ffn down; cross k, v on the text */
+        return 2.0 * n * (3 * d * inner + 3 * inner * d + f * d) +
+               2.0 * c->text_rows * (2 * d * inner);
+    /* qkv, out (the SwiGLU MLP is one class-ACT op) */
+    return 2.0 * n * (3 * d * inner + inner * d);
+}
+
+uint32_t h3hip_dit_block_plain_gemm_launches(const h3hip_dit_config *c) {
+    return c->family == H3HIP_FAMILY_WAN ? 7u : 2u;
+}
+
+int h3hip_dit_run_blocks_ops(h3hip_dit *dit, uint32_t first, uint32_t count,
+                             unsigned op_mask) {
     if (!dit) return 0;
+    dit->op_mask = op_mask;
     if (first > dit->config.blocks || count > dit->config.blocks - first)
         return dit_fail(dit, "block range [%u, %u) outside %u blocks", first,
                         first + count, dit->config.blocks);

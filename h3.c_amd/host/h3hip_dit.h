@@ -78,6 +78,24 @@ h3_gpu_tensor *h3hip_dit_tensor(h3hip_dit *dit, const char *name,
  * the next block is in the range (reference h3_dit.c:2139-2178). */
 int h3hip_dit_run_blocks(h3hip_dit *dit, uint32_t first, uint32_t count);
 
+/* Op classes of a block, for isolating one kernel family when timing:
+ * run_blocks_ops() issues only the ops whose class bit is set, in the same
+ * order and with the same shapes and tensors as run_blocks() (the numerics
+ * of a partial run are meaningless; the launches are identical). */
+enum {
+    H3HIP_OPS_GEMM = 1,      /* plain-epilogue projections (+bias) */
+    H3HIP_OPS_GEMM_ACT = 2,  /* projections with a SwiGLU / GELU epilogue */
+    H3HIP_OPS_ATTENTION = 4, /* flash attention (self and cross) */
+    H3HIP_OPS_ROWS = 8,      /* adaLN, gates, norms, RoPE, residual adds */
+    H3HIP_OPS_ALL = 15
+};
+int h3hip_dit_run_blocks_ops(h3hip_dit *dit, uint32_t first, uint32_t count,
+                             unsigned op_mask);
+/* FLOPs one block spends in the plain-epilogue projections (class GEMM). */
+double h3hip_dit_block_plain_gemm_flops(const h3hip_dit_config *config);
+/* Launches of class GEMM per block. */
+uint32_t h3hip_dit_block_plain_gemm_launches(const h3hip_dit_config *config);
+
 /* Algorithmic FLOPs of one block at the configured shape (GEMMs + attention,
  * 2 flops per multiply-add). */
 double h3hip_dit_block_flops(const h3hip_dit_config *config);
