@@ -5,6 +5,11 @@
     python h3.c_amd/rocprof_summary.py pmc <counter_collection.csv> <kernel-substring>
         per-dispatch average of every counter for the kernels matching the
         substring, and for the calibration kernel (hk_elementwise<2>, add_bf16)
+    python h3.c_amd/rocprof_summary.py traffic <fetch.csv> <write.csv> <kernel-substring> <calib-elements>
+        HBM-side bytes per launch of the matching kernel as JSON: FETCH_SIZE
+        and WRITE_SIZE (KiB per dispatch) scaled by what they read for the
+        last add_bf16 dispatch, which moves exactly 2 x 2 x calib-elements
+        bytes in and 2 x calib-elements bytes out
 """
 import csv
 import sqlite3
@@ -37,8 +42,54 @@ def pmc(path, match):
               f"avg {sum(vals) / len(vals):16.1f}")
 
 
+def _dispatches(path, match):
+    out = []
+    for r in csv.DictReader(open(path)):
+        if match in r["Kernel_Name"]:
+            out.append((int(r["Dispatch_Id"]), int(r["Grid_Size"]),
+                        float(r["Counter_Value"])))
+    return sorted(out)
+
+
+def traffic(fetch_csv, write_csv, match, calib_elements):
+    import json
+    calib_in = 4 * calib_elements
+    calib_out = 2 * calib_elements
+    f_cal = _dispatches(fetch_csv, "hk_elementwise<2>")[-1][2] * 1024
+    w_cal = _dispatches(write_csv, "hk_elementwise<2>")[-1][2] * 1024
+    f_scale, w_scale = calib_in / f_cal, calib_out / w_cal
+    fetch = _dispatches(fetch_csv, match)
+    write = _dispatches(write_csv, match)
+    per_grid = defaultdict(lambda: [0, 0.0, 0.0])
+    for (_, grid, fv), (_, _, wv) in zip(fetch, write):
+        e = per_grid[grid]
+        e[0] += 1
+        e[1] += fv * 1024 * f_scale
+        e[2] += wv * 1024 * w_scale
+    n = len(fetch)
+    total_f = sum(e[1] for e in per_grid.values())
+    total_w = sum(e[2] for e in per_grid.values())
+    print(json.dumps({
+        "kernel": match,
+        "dispatches": n,
+        "calibration": {"kernel": "hk_elementwise<2> (add_bf16)",
+                        "elements": calib_elements,
+                        "fetch_scale": round(f_scale, 5),
+                        "write_scale": round(w_scale, 5)},
+        "per_grid": {str(g): {"dispatches": e[0],
+                              "fetch_bytes": round(e[1] / e[0]),
+                              "write_bytes": round(e[2] / e[0])}
+                     for g, e in sorted(per_grid.items())},
+        "fetch_bytes_per_launch": round(total_f / n),
+        "write_bytes_per_launch": round(total_w / n),
+        "bytes_per_launch": round((total_f + total_w) / n),
+    }, indent=1))
+
+
 if __name__ == "__main__":
     if sys.argv[1] == "stats":
         stats(sys.argv[2], int(sys.argv[3]) if len(sys.argv) > 3 else 25)
+    elif sys.argv[1] == "traffic":
+        traffic(sys.argv[2], sys.argv[3], sys.argv[4], int(sys.argv[5]))
     else:
         pmc(sys.argv[2], sys.argv[3])
