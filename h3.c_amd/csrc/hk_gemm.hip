@@ -157,20 +157,26 @@ hk_gemm_mfma(hk_gemm_args g) {
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
-    auto issue_loads = [&](uint32_t stage, uint32_t k0) {
+    /* One 16-byte direct-to-LDS load: t in [0, 16) is the wave's t-th load
+     * of a stage, even t the X tile, odd t the W tile. */
+    auto issue_load = [&](uint32_t stage, uint32_t kb, int t) {
         uint8_t *sx = hk_smem + stage * HK_STAGE_BYTES;
-        uint8_t *sw = sx + HK_TILE_BYTES;
-        const uint32_t kb = k0 * 2u;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const uint32_t base = (wave * 8u + j) * 1024u;
+        const int j = t >> 1;
+        const uint32_t base = (wave * 8u + j) * 1024u;
+        if ((t & 1) == 0)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 xr, (__attribute__((address_space(3))) void *)(sx + base), 16,
                 x_off[j] + kb, 0, 0, 0);
+        else
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                wr, (__attribute__((address_space(3))) void *)(sw + base), 16,
-                w_off[j] + kb, 0, 0, 0);
-        }
+                wr,
+                (__attribute__((address_space(3))) void *)(sx + HK_TILE_BYTES +
+                                                           base),
+                16, w_off[j] + kb, 0, 0, 0);
+    };
+    auto issue_loads = [&](uint32_t stage, uint32_t k0) {
+#pragma unroll
+        for (int t = 0; t < 16; t++) issue_load(stage, k0 * 2u, t);
     };
 
     /* ---- main loop ----
@@ -178,9 +184,12 @@ hk_gemm_mfma(hk_gemm_args g) {
      * MFMAs that consume them; the matching s_waitcnt names the fragment
      * registers as operands, and sched_barrier(0) pins the read / MFMA /
      * wait phases so the scheduler cannot fold them back together.  The
-     * stage barrier sits before the last k-step: by then every wave holds
-     * all fragments of the current stage in registers, so the last 16 MFMAs
-     * overlap the first fragment reads of the next stage. */
+     * stage barrier sits before the last 16 MFMAs of a stage: by then every
+     * wave holds all of the stage's fragments in registers, so the stage's
+     * LDS is free.  The loads of the stage after next go into it right
+     * there, one after each of those 16 MFMAs: the load issue hides under
+     * the matrix pipe, and every load has a full stage (64 MFMAs per wave)
+     * plus a phase to land before the barrier that waits for it. */
     const uint32_t k_steps = g.k / HK_BK;
     const uint32_t frag_row = lane & 31u;
     const uint32_t frag_half = lane >> 5;
@@ -231,17 +240,32 @@ hk_gemm_mfma(hk_gemm_args g) {
                     __builtin_bit_cast(hk_bf16x8, fx[buf][j]), acc[i][j], 0,
                     0, 0);
     };
+    /* the last phase of a stage, with the loads of stage `load_stage` at
+     * k offset kb interleaved one per MFMA */
+    auto mfmas_loading = [&](int buf, uint32_t load_stage, uint32_t kb) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    __builtin_bit_cast(hk_bf16x8, fw[buf][i]),
+                    __builtin_bit_cast(hk_bf16x8, fx[buf][j]), acc[i][j], 0,
+                    0, 0);
+                issue_load(load_stage, kb, i * 4 + j);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+    };
 
     issue_loads(0, 0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    if (k_steps > 1) issue_loads(1, HK_BK);
     read_frags(0, 0, 0);
     wait_frags(0);
 #define HK_PIN() __builtin_amdgcn_sched_barrier(0)
     for (uint32_t kt = 0; kt < k_steps; kt++) {
         const uint32_t stage = kt & 1u;
         const bool more = kt + 1 < k_steps;
-        if (more) issue_loads(stage ^ 1u, (kt + 1) * HK_BK);
         read_frags(1, stage, 1);
         HK_PIN();
         mfmas(0);
@@ -258,12 +282,15 @@ hk_gemm_mfma(hk_gemm_args g) {
         HK_PIN();
         wait_frags(1);
         /* every wave now holds the whole stage in registers; the next stage
-         * is complete once every wave's DMA has landed */
+         * is complete once every wave's loads have landed */
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (more) read_frags(0, stage ^ 1u, 0);
         HK_PIN();
-        mfmas(1);
+        /* past the end the loads repeat the last stage (into LDS no one
+         * reads again), which keeps the loop free of branches around the
+         * accumulators */
+        mfmas_loading(1, stage, min(kt + 2, k_steps - 1) * HK_BK * 2u);
         HK_PIN();
         if (more) wait_frags(0);
     }
