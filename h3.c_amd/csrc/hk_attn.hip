@@ -24,7 +24,12 @@
  *     double-buffered LDS (2 x 33 KiB) with the next tile's global loads in
  *     flight during the current tile's 64 MFMAs per wave;
  *   - the grid is 1-D and regrouped per XCD so the query blocks of one head
- *     run on one XCD and share its L2 copy of that head's K and V.
+ *     run on one XCD and share its L2 copy of that head's K and V;
+ *   - the softmax is VALU-bound, so its instruction count is kept low: the
+ *     running max only moves (rescaling O and l) when a tile's max exceeds
+ *     it by more than 2^8, the scale is folded into one FMA per score, row
+ *     maxima use v_max3, and the key-range mask is compiled only into the
+ *     last tile's step.
  *
  * A two-pass reference kernel (the reference's naive SDPA,
  * h3_cuda_attention.cu:488-549: one workgroup per (row, head), normalised
@@ -34,6 +39,7 @@
 #include "hk_internal.h"
 
 #include <math.h>
+#include <type_traits>
 
 #define HK_HD 128
 #define HK_QB 256             /* queries per workgroup */
@@ -156,7 +162,8 @@ __global__ void __launch_bounds__(256, 1) hk_flash_fwd(hk_attn_args a) {
     store_tile(0);
     __syncthreads();
 
-    for (uint32_t t = 0; t < tiles; t++) {
+    auto tile_step = [&](uint32_t t, auto tail_tag) {
+        constexpr bool tail = decltype(tail_tag)::value;
         const uint32_t stage = t & 1u;
         if (t + 1 < tiles) load_tile((t + 1) * HK_KT);
         const uint8_t *ks = hk_lds + stage * HK_STAGE_BYTES;
@@ -183,38 +190,55 @@ __global__ void __launch_bounds__(256, 1) hk_flash_fwd(hk_attn_args a) {
             }
         }
 
-        /* online softmax per query column */
+        /* online softmax per query column.  The running maximum is only
+         * moved (and O, l rescaled) when a score exceeds it by more than
+         * 2^8 in the exp2 domain; otherwise P = exp2(s - m_stale) <= 256.
+         * A power-of-two offset commutes with bf16 rounding, so P and the
+         * final O / l match an every-tile rescale up to f32 rounding. */
         const uint32_t kv0 = t * HK_KT;
-        const bool tail = kv0 + HK_KT > a.kv_rows;
         hk_bf16x8 pf[2][2][2]; /* [kt][step][g] */
 #pragma unroll
         for (int g = 0; g < 2; g++) {
             float mx = -INFINITY;
+            if constexpr (tail) {
+#pragma unroll
+                for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const uint32_t key = kv0 + kt * 32u + (r >> 2) * 8u +
+                                             half * 4u + (r & 3);
+                        if (key >= a.kv_rows) s[kt][g][r] = -INFINITY;
+                    }
+            }
 #pragma unroll
             for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    float v = s[kt][g][r] * a.scale_log2;
-                    if (tail) {
-                        const uint32_t key = kv0 + kt * 32u + (r >> 2) * 8u +
-                                             half * 4u + (r & 3);
-                        if (key >= a.kv_rows) v = -INFINITY;
-                    }
-                    s[kt][g][r] = v;
-                    mx = fmaxf(mx, v);
-                }
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float m_new = fmaxf(m_run[g], mx);
-            const float ref = m_new == -INFINITY ? 0.0f : m_new;
-            const float c = __builtin_amdgcn_exp2f(m_run[g] - ref);
-            m_run[g] = m_new;
+                for (int r = 0; r < 16; r += 2)
+                    asm("v_max3_f32 %0, %0, %1, %2"
+                        : "+v"(mx)
+                        : "v"(s[kt][g][r]), "v"(s[kt][g][r + 1]));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * a.scale_log2;
+            const bool grow = mx > m_run[g] + 8.0f;
+            if (__builtin_amdgcn_ballot_w64(grow)) {
+                const float m_new = fmaxf(m_run[g], mx);
+                const float ref = m_new == -INFINITY ? 0.0f : m_new;
+                const float c = __builtin_amdgcn_exp2f(m_run[g] - ref);
+                m_run[g] = ref;
+                l_part[g] *= c;
+#pragma unroll
+                for (int d = 0; d < 4; d++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) o[d][g][r] *= c;
+            }
+            const float neg = -m_run[g];
             float sum = 0.0f;
 #pragma unroll
             for (int kt = 0; kt < 2; kt++) {
                 float p[16];
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    p[r] = __builtin_amdgcn_exp2f(s[kt][g][r] - ref);
+                    p[r] = __builtin_amdgcn_exp2f(
+                        __builtin_fmaf(s[kt][g][r], a.scale_log2, neg));
                     sum += p[r];
                 }
 #pragma unroll
@@ -225,11 +249,7 @@ __global__ void __launch_bounds__(256, 1) hk_flash_fwd(hk_attn_args a) {
                     pf[kt][st][g] = v;
                 }
             }
-            l_part[g] = l_part[g] * c + sum;
-#pragma unroll
-            for (int d = 0; d < 4; d++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) o[d][g][r] *= c;
+            l_part[g] += sum;
         }
 
         /* O^T[d][g] += V^T[d, keys] . P^T[keys, g] */
@@ -254,7 +274,10 @@ __global__ void __launch_bounds__(256, 1) hk_flash_fwd(hk_attn_args a) {
 
         if (t + 1 < tiles) store_tile(stage ^ 1u);
         __syncthreads();
-    }
+    };
+    for (uint32_t t = 0; t + 1 < tiles; t++)
+        tile_step(t, std::integral_constant<bool, false>());
+    tile_step(tiles - 1, std::integral_constant<bool, true>());
 
     /* ---- normalise and store: lane owns query column `col` of group g and
      * dims d*32 + (r/4)*8 + 4*half + r%4 */

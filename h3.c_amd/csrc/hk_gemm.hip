@@ -230,30 +230,35 @@ hk_gemm_mfma(hk_gemm_args g) {
                        "+v"(fw[buf][3]), "+v"(fx[buf][0]), "+v"(fx[buf][1]),
                        "+v"(fx[buf][2]), "+v"(fx[buf][3]));
     };
-    auto mfmas = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                    __builtin_bit_cast(hk_bf16x8, fw[buf][i]),
-                    __builtin_bit_cast(hk_bf16x8, fx[buf][j]), acc[i][j], 0,
-                    0, 0);
+    /* one fragment read: idx 0-3 the W fragments, 4-7 the X fragments */
+    auto read_one = [&](int buf, uint32_t stage, int ks, int idx) {
+        const uint32_t so = stage * HK_STAGE_BYTES + chunk_off[ks];
+        if (idx < 4)
+            asm volatile("ds_read_b128 %0, %1 offset:%2"
+                         : "=&v"(fw[buf][idx])
+                         : "v"(w_row_base + so), "i"(idx * 4096));
+        else
+            asm volatile("ds_read_b128 %0, %1 offset:%2"
+                         : "=&v"(fx[buf][idx - 4])
+                         : "v"(x_row_base + so), "i"((idx - 4) * 4096));
     };
-    /* the last phase of a stage, with the loads of stage `load_stage` at
-     * k offset kb interleaved one per MFMA */
-    auto mfmas_loading = [&](int buf, uint32_t load_stage, uint32_t kb) {
+    /* One k-substep: 16 MFMAs on buffer `buf`, with the next substep's 8
+     * fragment reads (into the other buffer) spread one per two MFMAs and,
+     * in the last substep of a stage, the 16 loads of the stage after next
+     * one per MFMA. */
+    auto substep = [&](int buf, uint32_t rstage, int rks, bool loading,
+                       uint32_t lstage, uint32_t kb) {
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                    __builtin_bit_cast(hk_bf16x8, fw[buf][i]),
-                    __builtin_bit_cast(hk_bf16x8, fx[buf][j]), acc[i][j], 0,
-                    0, 0);
-                issue_load(load_stage, kb, i * 4 + j);
-                __builtin_amdgcn_sched_barrier(0);
-            }
+        for (int t = 0; t < 16; t++) {
+            const int i = t >> 2, j = t & 3;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(hk_bf16x8, fw[buf][i]),
+                __builtin_bit_cast(hk_bf16x8, fx[buf][j]), acc[i][j], 0, 0,
+                0);
+            if (t & 1) read_one(buf ^ 1, rstage, rks, t >> 1);
+            if (loading) issue_load(lstage, kb, t);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     };
 
     issue_loads(0, 0);
@@ -265,34 +270,23 @@ hk_gemm_mfma(hk_gemm_args g) {
 #define HK_PIN() __builtin_amdgcn_sched_barrier(0)
     for (uint32_t kt = 0; kt < k_steps; kt++) {
         const uint32_t stage = kt & 1u;
-        const bool more = kt + 1 < k_steps;
-        read_frags(1, stage, 1);
-        HK_PIN();
-        mfmas(0);
-        HK_PIN();
+        substep(0, stage, 1, false, 0, 0);
         wait_frags(1);
-        read_frags(0, stage, 2);
-        HK_PIN();
-        mfmas(1);
-        HK_PIN();
+        substep(1, stage, 2, false, 0, 0);
         wait_frags(0);
-        read_frags(1, stage, 3);
-        HK_PIN();
-        mfmas(0);
-        HK_PIN();
+        substep(0, stage, 3, false, 0, 0);
         wait_frags(1);
         /* every wave now holds the whole stage in registers; the next stage
          * is complete once every wave's loads have landed */
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (more) read_frags(0, stage ^ 1u, 0);
         HK_PIN();
-        /* past the end the loads repeat the last stage (into LDS no one
-         * reads again), which keeps the loop free of branches around the
+        /* past the end the reads and loads repeat a stage no one uses
+         * again, which keeps the loop free of branches around the
          * accumulators */
-        mfmas_loading(1, stage, min(kt + 2, k_steps - 1) * HK_BK * 2u);
-        HK_PIN();
-        if (more) wait_frags(0);
+        substep(1, stage ^ 1u, 0, true, stage,
+                min(kt + 2, k_steps - 1) * HK_BK * 2u);
+        wait_frags(0);
     }
 #undef HK_PIN
 

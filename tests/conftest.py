@@ -47,7 +47,7 @@ def to_f32(bits):
 
 
 def assert_close(got_bits, want_bits, atol=1e-3, rtol=1e-2, what="",
-                 chained=0):
+                 chained=0, extra_abs=None):
     """The reference's GEMM / flash tolerance: |g - r| <= atol + rtol |r|
     (tests/test_cuda_dit.c:73-91, tests/test_cuda_attention.c:79-114).
 
@@ -60,11 +60,31 @@ def assert_close(got_bits, want_bits, atol=1e-3, rtol=1e-2, what="",
     r = to_f32(want_bits).astype(np.float64)
     err = np.abs(g - r)
     extra = chained * 4 * 2.0 ** -8 * np.sqrt(np.mean(r * r)) if r.size else 0
+    if extra_abs is not None:
+        extra = extra + np.asarray(extra_abs, dtype=np.float64).reshape(-1)
     bad = err > atol + rtol * np.abs(r) + extra
     assert not np.isnan(g).any(), f"{what}: NaN in output"
     assert int(bad.sum()) == 0, (
         f"{what}: {int(bad.sum())}/{g.size} beyond tolerance, "
         f"max err {err.max():.3g}")
+
+
+def sdpa_p_rounding_bound(q, k, v, q_rows, kv_rows, heads, hd, scale,
+                          head_major=False):
+    """Per-output bound on what rounding P to bf16 can move an attention
+    output: flash kernels round P relative to their own running maximum
+    (a tile's, or a stale one within 2^8), the oracle relative to the row's
+    global maximum; the two roundings of one P differ by at most one bf16
+    ulp, 2^-8 relative, so |O_a - O_b| <= 2^-8 sum_j p_j |v_j| / sum_j p_j.
+    Computed in float64 from the bf16 inputs."""
+    Q = to_f32(q).astype(np.float64).reshape(q_rows, heads, hd)
+    K = to_f32(k).astype(np.float64).reshape(kv_rows, heads, hd)
+    V = np.abs(to_f32(v).astype(np.float64).reshape(kv_rows, heads, hd))
+    s = np.einsum("qhd,khd->hqk", Q, K) * scale
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    b = 2.0 ** -8 * np.einsum("hqk,khd->hqd", p, V)
+    return b if head_major else b.transpose(1, 0, 2)
 
 
 def cosine_rel_l2(got_bits, want_bits):

@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 
 from conftest import (adaln_terms, assert_close, assert_row_close,
+                      sdpa_p_rounding_bound,
                       assert_ulp, rand_bf16, to_f32)
 
 pytestmark = pytest.mark.gpu
@@ -273,7 +274,9 @@ def test_sdpa(gpu, q_rows, kv_rows, heads):
     else:
         gpu.run("h3_gpu_sdpa_cross_bf16", out, gpu.bf16(q), gpu.bf16(k),
                 gpu.bf16(v), q_rows, kv_rows, heads, hd, C.c_float(scale))
-    assert_close(gpu.read_bf16(out), want, what=f"SDPA {q_rows}x{kv_rows}")
+    assert_close(gpu.read_bf16(out), want, what=f"SDPA {q_rows}x{kv_rows}",
+                 extra_abs=sdpa_p_rounding_bound(q, k, v, q_rows, kv_rows,
+                                                 heads, hd, scale))
 
 
 def test_sdpa_head_major(gpu):
@@ -285,7 +288,9 @@ def test_sdpa_head_major(gpu):
     out = gpu.new_bf16(n * heads * hd)
     gpu.run("h3_gpu_sdpa_bf16_head_major_output", out, gpu.bf16(q),
             gpu.bf16(k), gpu.bf16(v), n, heads, hd, C.c_float(scale))
-    assert_close(gpu.read_bf16(out), want, what="head-major SDPA")
+    assert_close(gpu.read_bf16(out), want, what="head-major SDPA",
+                 extra_abs=sdpa_p_rounding_bound(q, k, v, n, n, heads, hd,
+                                                 scale, head_major=True))
 
 
 def test_sdpa_constant_keys_give_mean_value(gpu):
