@@ -58,29 +58,6 @@ def rope_tables(positions):
     return cos, sin
 
 
-def h3_layout_rows(text_len, latent_t, latent_h, latent_w, audio_t):
-    """Packed H3 sequence (text, audio, video) with its positions and the
-    step-0 row map of the serving schedule."""
-    L = h3hip.lib()
-    lay = h3hip.Layout()
-    err = __import__("ctypes").create_string_buffer(256)
-    ok = L.h3hip_layout_build(text_len, latent_t, latent_h, latent_w, audio_t,
-                              22, None, 0, None, 0,
-                              __import__("ctypes").byref(lay), err, 256)
-    if not ok:
-        raise RuntimeError(err.value.decode())
-    n = lay.seq_len
-    pos = np.array([[lay.positions[i].t, lay.positions[i].h,
-                     lay.positions[i].w] for i in range(n)])
-    segs = [(lay.segments[i].start, lay.segments[i].stop,
-             lay.segments[i].kind) for i in range(lay.segment_count)]
-    L.h3hip_layout_free(__import__("ctypes").byref(lay))
-    row_map = np.zeros(n, np.uint32)
-    for start, stop, kind in segs:       # video row 0 / audio row 1 at step 0
-        row_map[start:stop] = {0: 1, 4: 1 * 3 + 2, 5: 0}.get(kind, 0)
-    return n, pos, row_map
-
-
 def time_forward(gpu, dit, blocks, steps, warmup):
     for _ in range(warmup):
         dit.run_blocks(0, blocks)
@@ -142,6 +119,68 @@ def profile_pass(gpu, dit, blocks):
     gpu.check(L.h3_gpu_add_bf16(gpu.h, c, a, b, n), "calibration add")
     gpu.submit()
     log("profile pass done")
+
+
+def h3_measure(gpu, blocks, reps):
+    """The H3 block at its real 512x512x22f shape (512 text + 74 audio +
+    1792 video rows): one 50-block forward, and BASELINE config 5, the
+    20-step serving-schedule Euler denoise with velocity reuse 2 (11 fresh
+    forwards, extrapolated skipped steps), end to end on the GPU: patch
+    projection, packing, blocks, final adaLN heads, Euler updates."""
+    import ctypes as C
+    L = h3hip.lib()
+    lay = h3hip.Layout()
+    err = C.create_string_buffer(256)
+    if not L.h3hip_layout_build(512, 7, 32, 32, 37, 22, None, 0, None, 0,
+                                C.byref(lay), err, 256):
+        raise RuntimeError(err.value.decode())
+    n = lay.seq_len
+    pos = np.array([[lay.positions[i].t, lay.positions[i].h,
+                     lay.positions[i].w] for i in range(n)])
+    steps = 20
+    v_sig = np.zeros(steps + 1, np.float32)
+    a_sig = np.zeros(steps + 1, np.float32)
+    L.h3hip_serving_schedule_build(steps, h3hip.ptr(v_sig), h3hip.ptr(a_sig))
+    vr = np.zeros(steps, np.uint32)
+    ar = np.zeros(steps, np.uint32)
+    time_rows = L.h3hip_time_rows(steps, h3hip.ptr(v_sig), h3hip.ptr(a_sig),
+                                  0, 0, h3hip.ptr(vr), h3hip.ptr(ar), None,
+                                  None, None)
+    hcfg = h3hip.dit_config(h3hip.FAMILY_H3, 5376, 56, 14336, n,
+                            blocks=blocks, time_rows=time_rows)
+    hdit = h3hip.Dit(gpu, hcfg)
+    try:
+        hdit.init_random(seed=1, weight_std=0.02, mod_std=0.1)
+        hc, hs = rope_tables(pos)
+        hdit.set_rope(hc, hs)
+        hdit.sampler_create(lay, v_sig, a_sig, reuse_interval=2)
+        hdit.sampler_init_random(seed=2, weight_std=0.02, mod_std=0.1)
+        # forward alone, on the step-0 modulation rows
+        hdit.gpu.begin()
+        if not L.h3hip_dit_forward_step(hdit.h, 0):
+            raise RuntimeError(hdit.error())
+        hdit.gpu.submit()
+        hms, _ = time_forward(gpu, hdit, blocks, reps, 1)
+        hflops = hdit.block_flops()
+        real = {"rows": int(n), "s_per_forward": round(hms / 1e3, 4),
+                "ms_per_block": round(hms / blocks, 3),
+                "tflops": round(blocks * hflops / (hms / 1e3) / 1e12, 1)}
+        t0 = time.perf_counter()
+        evaluations = hdit.denoise()
+        seconds = time.perf_counter() - t0
+        v_out, a_out = hdit.read_latents()
+        if not (np.isfinite(v_out).all() and np.isfinite(a_out).all()):
+            raise RuntimeError("denoise produced non-finite latents")
+        den = {"config": "BASELINE config 5: 20-step serving-schedule Euler "
+                         "denoise, velocity reuse 2, H3 512x512x22f "
+                         "(2378 rows), 50 blocks",
+               "steps": steps, "fresh_forwards": int(evaluations),
+               "seconds": round(seconds, 3),
+               "s_per_fresh_forward": round(seconds / evaluations, 4)}
+    finally:
+        hdit.close()
+        L.h3hip_layout_free(C.byref(lay))
+    return real, den
 
 
 def load_traffic(name):
@@ -265,21 +304,10 @@ def main():
     dit.close()
 
     h3_real = None
+    denoise = None
     if not args.no_h3:
-        n, pos, row_map = h3_layout_rows(512, 7, 32, 32, 37)
-        hcfg = h3hip.dit_config(h3hip.FAMILY_H3, 5376, 56, 14336, n,
-                                blocks=blocks, time_rows=2)
-        hdit = h3hip.Dit(gpu, hcfg)
-        hdit.init_random(seed=1, weight_std=0.02, mod_std=0.1)
-        hc, hs = rope_tables(pos)
-        hdit.set_rope(hc, hs)
-        hdit.set_row_map(row_map)
-        hms, _ = time_forward(gpu, hdit, blocks, max(2, args.steps // 2), 1)
-        hflops = hdit.block_flops()
-        h3_real = {"rows": int(n), "s_per_forward": round(hms / 1e3, 4),
-                   "ms_per_block": round(hms / blocks, 3),
-                   "tflops": round(blocks * hflops / (hms / 1e3) / 1e12, 1)}
-        hdit.close()
+        log("H3 real shape: forward + 20-step Euler denoise ...")
+        h3_real, denoise = h3_measure(gpu, blocks, max(2, args.steps // 2))
 
     base = None
     if not args.no_cpu_baseline:
@@ -342,6 +370,7 @@ def main():
                      "avg_launch_us": round(per_launch_ms * 1e3, 1),
                      "traffic": load_traffic("gemm_plain_wan512_traffic.json")},
         "h3_real_shape": h3_real,
+        "denoise": denoise,
         "cpu_baseline": base,
     }
     gpu.close()

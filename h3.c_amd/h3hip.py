@@ -50,6 +50,13 @@ class Layout(C.Structure):
                 ("audio_cond_rows", _SZ), ("audio_target_rows", _SZ)]
 
 
+class SamplerConfig(C.Structure):
+    _fields_ = [("layout", C.POINTER(Layout)), ("steps", _I),
+                ("video_sigmas", C.POINTER(_F)),
+                ("audio_sigmas", C.POINTER(_F)), ("reuse_interval", _I),
+                ("video_patch", _U32), ("audio_channels", _U32)]
+
+
 class Rng(C.Structure):
     _fields_ = [("state", C.c_uint64), ("increment", C.c_uint64),
                 ("spare", _F), ("has_spare", _I)]
@@ -176,6 +183,15 @@ def lib():
         "h3hip_dit_block_attention_flops": (C.c_double,
                                             [C.POINTER(DitConfig)]),
         "h3hip_dit_error": (C.c_char_p, [_P]),
+        "h3hip_dit_sampler_create": (_I, [_P, C.POINTER(SamplerConfig)]),
+        "h3hip_dit_sampler_init_random": (_I, [_P, C.c_uint64, _F, _F]),
+        "h3hip_dit_sampler_write_latents": (_I, [_P, _P, _P]),
+        "h3hip_dit_sampler_read_latents": (_I, [_P, _P, _P]),
+        "h3hip_dit_forward_step": (_I, [_P, _I]),
+        "h3hip_dit_denoise": (_I, [_P]),
+        "h3hip_dit_sampler_rows": (None, [_P, C.POINTER(_U32),
+                                          C.POINTER(_U32), C.POINTER(_U32),
+                                          C.POINTER(_U32)]),
         # host math
         "h3hip_temporal": (None, [_I, C.POINTER(_I), C.POINTER(_I),
                                   C.POINTER(_I)]),
@@ -418,6 +434,63 @@ class Dit:
 
     def block_flops(self):
         return self.gpu.L.h3hip_dit_block_flops(C.byref(self.cfg))
+
+    # ---- H3 sampler (h3hip_dit.h) ----
+    def sampler_create(self, layout, video_sigmas, audio_sigmas,
+                       reuse_interval=1, video_patch=96, audio_channels=32):
+        """layout: a Layout structure (kept alive by the caller)."""
+        steps = len(video_sigmas) - 1
+        self._sig = (np.ascontiguousarray(video_sigmas, dtype=np.float32),
+                     np.ascontiguousarray(audio_sigmas, dtype=np.float32))
+        cfg = SamplerConfig(C.pointer(layout), steps,
+                            self._sig[0].ctypes.data_as(C.POINTER(_F)),
+                            self._sig[1].ctypes.data_as(C.POINTER(_F)),
+                            reuse_interval, video_patch, audio_channels)
+        if not self.gpu.L.h3hip_dit_sampler_create(self.h, C.byref(cfg)):
+            raise RuntimeError(self.error())
+        self.video_patch, self.audio_channels = video_patch, audio_channels
+
+    def sampler_rows(self):
+        v, a, vt, at = _U32(), _U32(), _U32(), _U32()
+        self.gpu.L.h3hip_dit_sampler_rows(self.h, C.byref(v), C.byref(a),
+                                          C.byref(vt), C.byref(at))
+        return v.value, a.value, vt.value, at.value
+
+    def sampler_init_random(self, seed, weight_std=0.02, mod_std=0.02):
+        if not self.gpu.L.h3hip_dit_sampler_init_random(self.h, seed,
+                                                        weight_std, mod_std):
+            raise RuntimeError(self.error())
+
+    def write_latents(self, video, audio):
+        v = np.ascontiguousarray(video, dtype=np.float32)
+        a = np.ascontiguousarray(audio, dtype=np.float32)
+        if not self.gpu.L.h3hip_dit_sampler_write_latents(self.h, ptr(v),
+                                                          ptr(a)):
+            raise RuntimeError(self.error())
+
+    def read_latents(self):
+        vr, ar, _, _ = self.sampler_rows()
+        v = np.empty(vr * self.video_patch, dtype=np.float32)
+        a = np.empty(ar * self.audio_channels, dtype=np.float32)
+        if not self.gpu.L.h3hip_dit_sampler_read_latents(self.h, ptr(v),
+                                                         ptr(a)):
+            raise RuntimeError(self.error())
+        return v, a
+
+    def forward_step(self, step, submit=True):
+        self.gpu.begin()
+        if not self.gpu.L.h3hip_dit_forward_step(self.h, step):
+            msg = self.error()
+            self.gpu.L.h3_gpu_submit(self.gpu.h)
+            raise RuntimeError(msg)
+        if submit:
+            self.gpu.submit()
+
+    def denoise(self):
+        n = self.gpu.L.h3hip_dit_denoise(self.h)
+        if not n:
+            raise RuntimeError(self.error())
+        return n
 
 
 def dit_config(family, hidden, heads, ffn, rows, blocks=1, text_rows=0,

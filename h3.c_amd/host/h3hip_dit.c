@@ -29,6 +29,28 @@ struct h3hip_dit {
     h3_gpu_tensor *cross_q, *cross_k, *cross_v, *cross_out, *ffn_act;
     int attention_adaln_ready;
     unsigned op_mask;
+    /* H3 sampler */
+    int sampler;
+    int steps, reuse_interval;
+    uint32_t video_patch, audio_channels;
+    float *video_sigmas, *audio_sigmas;
+    h3hip_segment *segments;
+    size_t segment_count;
+    uint32_t video_total, audio_total;       /* latent rows per modality */
+    uint32_t video_conditions, audio_conditions;
+    uint32_t video_targets, audio_targets;
+    uint32_t video_target_start, audio_target_start; /* rows in hidden */
+    h3_gpu_tensor *video_input, *audio_input; /* F32 latent rows */
+    h3_gpu_tensor *video_patch_w, *video_patch_b; /* F32 */
+    h3_gpu_tensor *audio_patch_w, *audio_patch_b;
+    h3_gpu_tensor *refined_text, *final_norm, *final_mod;
+    h3_gpu_tensor *final_video_w, *final_video_b;
+    h3_gpu_tensor *final_audio_w, *final_audio_b;
+    h3_gpu_tensor *video_velocity, *audio_velocity;
+    h3_gpu_tensor *video_previous, *audio_previous;
+    h3_gpu_tensor *video_inverse, *audio_inverse;
+    h3_gpu_tensor **step_maps, **final_video_maps, **final_audio_maps;
+    h3_gpu_tensor *default_row_map;
     char error[512];
 };
 
@@ -187,6 +209,8 @@ h3hip_dit *h3hip_dit_create(h3_gpu *gpu, const h3hip_dit_config *config,
     return dit;
 }
 
+static void sampler_free(h3hip_dit *dit);
+
 void h3hip_dit_free(h3hip_dit *dit) {
     if (!dit) return;
     if (dit->blocks) {
@@ -197,6 +221,8 @@ void h3hip_dit_free(h3hip_dit *dit) {
         }
         free(dit->blocks);
     }
+    /* a forward that failed mid-way may have left a step map installed */
+    if (dit->default_row_map) dit->row_map = dit->default_row_map;
     h3_gpu_tensor *shared[] = {
         dit->hidden, dit->row_map, dit->rope_cos, dit->rope_sin,
         dit->context, dit->mod_a, dit->mod_b, dit->qkv, dit->query,
@@ -204,6 +230,7 @@ void h3hip_dit_free(h3hip_dit *dit) {
         dit->cross_k, dit->cross_v, dit->cross_out, dit->ffn_act};
     for (size_t i = 0; i < sizeof(shared) / sizeof(*shared); i++)
         h3_gpu_tensor_free(shared[i]);
+    sampler_free(dit);
     free(dit);
 }
 
@@ -215,6 +242,33 @@ h3_gpu_tensor *h3hip_dit_tensor(h3hip_dit *dit, const char *name,
     if (!strcmp(name, "rope_cos")) return dit->rope_cos;
     if (!strcmp(name, "rope_sin")) return dit->rope_sin;
     if (!strcmp(name, "context")) return dit->context;
+    if (dit->sampler) {
+        struct { const char *name; h3_gpu_tensor *tensor; } shared[] = {
+            {"video_input", dit->video_input},
+            {"audio_input", dit->audio_input},
+            {"video_patch_w", dit->video_patch_w},
+            {"video_patch_b", dit->video_patch_b},
+            {"audio_patch_w", dit->audio_patch_w},
+            {"audio_patch_b", dit->audio_patch_b},
+            {"refined_text", dit->refined_text},
+            {"final_norm", dit->final_norm},
+            {"final_modulation", dit->final_mod},
+            {"final_video_w", dit->final_video_w},
+            {"final_video_b", dit->final_video_b},
+            {"final_audio_w", dit->final_audio_w},
+            {"final_audio_b", dit->final_audio_b},
+            {"video_velocity", dit->video_velocity},
+            {"audio_velocity", dit->audio_velocity}};
+        for (size_t i = 0; i < sizeof(shared) / sizeof(*shared); i++)
+            if (!strcmp(name, shared[i].name)) return shared[i].tensor;
+        if ((int)block < dit->steps) {
+            if (!strcmp(name, "step_row_map")) return dit->step_maps[block];
+            if (!strcmp(name, "final_video_map"))
+                return dit->final_video_maps[block];
+            if (!strcmp(name, "final_audio_map"))
+                return dit->final_audio_maps[block];
+        }
+    }
     if (block >= dit->config.blocks) return NULL;
     h3hip_block *w = &dit->blocks[block];
     struct { const char *name; h3_gpu_tensor *tensor; } table[] = {
@@ -313,6 +367,7 @@ int h3hip_dit_set_row_map(h3hip_dit *dit, const uint32_t *row_map) {
         h3_gpu_tensor_from_u32(dit->gpu, row_map, dit->config.rows);
     if (!fresh)
         return dit_fail(dit, "row map upload: %s", h3_gpu_error(dit->gpu));
+    if (dit->default_row_map == dit->row_map) dit->default_row_map = fresh;
     h3_gpu_tensor_free(dit->row_map);
     dit->row_map = fresh;
     return 1;
@@ -518,4 +573,436 @@ int h3hip_dit_run_blocks_ops(h3hip_dit *dit, uint32_t first, uint32_t count,
         if (!ok) return 0;
     }
     return 1;
+}
+
+/* ----------------------------------------------------------- sampler */
+
+static void free_maps(h3_gpu_tensor **maps, int count) {
+    if (!maps) return;
+    for (int i = 0; i < count; i++) h3_gpu_tensor_free(maps[i]);
+    free(maps);
+}
+
+static void sampler_free(h3hip_dit *dit) {
+    h3_gpu_tensor *owned[] = {
+        dit->video_input, dit->audio_input, dit->video_patch_w,
+        dit->video_patch_b, dit->audio_patch_w, dit->audio_patch_b,
+        dit->refined_text, dit->final_norm, dit->final_mod,
+        dit->final_video_w, dit->final_video_b, dit->final_audio_w,
+        dit->final_audio_b, dit->video_velocity, dit->audio_velocity,
+        dit->video_previous, dit->audio_previous, dit->video_inverse,
+        dit->audio_inverse};
+    for (size_t i = 0; i < sizeof(owned) / sizeof(*owned); i++)
+        h3_gpu_tensor_free(owned[i]);
+    free_maps(dit->step_maps, dit->steps);
+    free_maps(dit->final_video_maps, dit->steps);
+    free_maps(dit->final_audio_maps, dit->steps);
+    free(dit->video_sigmas);
+    free(dit->audio_sigmas);
+    free(dit->segments);
+}
+
+static int is_video_kind(int kind) {
+    return kind == H3HIP_SEG_COND || kind == H3HIP_SEG_REF_IMAGE ||
+           kind == H3HIP_SEG_VIDEO;
+}
+
+static int is_audio_kind(int kind) {
+    return kind == H3HIP_SEG_REF_AUDIO || kind == H3HIP_SEG_AUDIO;
+}
+
+void h3hip_dit_sampler_rows(const h3hip_dit *dit, uint32_t *video_rows,
+                            uint32_t *audio_rows, uint32_t *video_targets,
+                            uint32_t *audio_targets) {
+    if (video_rows) *video_rows = dit ? dit->video_total : 0;
+    if (audio_rows) *audio_rows = dit ? dit->audio_total : 0;
+    if (video_targets) *video_targets = dit ? dit->video_targets : 0;
+    if (audio_targets) *audio_targets = dit ? dit->audio_targets : 0;
+}
+
+int h3hip_dit_sampler_create(h3hip_dit *dit,
+                             const h3hip_sampler_config *cfg) {
+    if (!dit) return 0;
+    if (dit->sampler) return dit_fail(dit, "sampler already created");
+    const h3hip_dit_config *c = &dit->config;
+    if (is_wan(dit))
+        return dit_fail(dit, "the sampler drives the H3 block family");
+    if (!cfg || !cfg->layout || cfg->steps < 1 || !cfg->video_sigmas ||
+        !cfg->audio_sigmas || cfg->reuse_interval < 1 ||
+        cfg->reuse_interval > 32 || !cfg->video_patch ||
+        !cfg->audio_channels)
+        return dit_fail(dit, "invalid sampler configuration");
+    const h3hip_layout *layout = cfg->layout;
+    if (layout->seq_len != c->rows)
+        return dit_fail(dit, "layout has %zu rows, the DiT %u",
+                        layout->seq_len, c->rows);
+    /* time rows of this schedule (reference h3_dit_schedule.c:78-161) */
+    const int steps = cfg->steps;
+    uint32_t *video_time = (uint32_t *)calloc(steps, sizeof(uint32_t));
+    uint32_t *audio_time = (uint32_t *)calloc(steps, sizeof(uint32_t));
+    uint32_t *visual_time = (uint32_t *)calloc(steps, sizeof(uint32_t));
+    uint32_t *audio_cond_time = (uint32_t *)calloc(steps, sizeof(uint32_t));
+    if (!video_time || !audio_time || !visual_time || !audio_cond_time) {
+        free(video_time); free(audio_time); free(visual_time);
+        free(audio_cond_time);
+        return dit_fail(dit, "out of memory");
+    }
+    int visual_condition = 0, audio_condition = 0;
+    uint32_t video_total = 0, audio_total = 0;
+    uint32_t video_targets = 0, audio_targets = 0;
+    uint32_t video_conditions = 0, audio_conditions = 0;
+    uint32_t video_start = 0, audio_start = 0, text_rows = 0;
+    int video_segments = 0, audio_segments = 0, ok = 1;
+    for (size_t i = 0; i < layout->segment_count && ok; i++) {
+        const h3hip_segment *seg = &layout->segments[i];
+        uint32_t n = (uint32_t)(seg->stop - seg->start);
+        if (seg->kind == H3HIP_SEG_TEXT) {
+            text_rows += n;
+        } else if (is_video_kind(seg->kind)) {
+            if (seg->kind == H3HIP_SEG_VIDEO) {
+                video_segments++;
+                video_targets = n;
+                video_start = (uint32_t)seg->start;
+                video_conditions = video_total;
+            } else {
+                visual_condition = 1;
+                if (video_segments) ok = 0; /* conditions precede targets */
+            }
+            video_total += n;
+        } else if (is_audio_kind(seg->kind)) {
+            if (seg->kind == H3HIP_SEG_AUDIO) {
+                audio_segments++;
+                audio_targets = n;
+                audio_start = (uint32_t)seg->start;
+                audio_conditions = audio_total;
+            } else {
+                audio_condition = 1;
+                if (audio_segments) ok = 0;
+            }
+            audio_total += n;
+        } else {
+            ok = 0;
+        }
+    }
+    uint32_t time_rows = ok ? h3hip_time_rows(
+        steps, cfg->video_sigmas, cfg->audio_sigmas, visual_condition,
+        audio_condition, video_time, audio_time, visual_time,
+        audio_cond_time, NULL) : 0;
+    if (!ok || video_segments != 1 || audio_segments != 1 || !time_rows ||
+        time_rows != c->time_rows) {
+        free(video_time); free(audio_time); free(visual_time);
+        free(audio_cond_time);
+        if (!ok || video_segments != 1 || audio_segments != 1)
+            return dit_fail(dit, "the layout needs one video and one audio "
+                                 "target segment after their conditions");
+        return dit_fail(dit, "the schedule has %u time rows, the DiT "
+                             "modulation %u", time_rows, c->time_rows);
+    }
+    dit->steps = steps;
+    dit->reuse_interval = cfg->reuse_interval;
+    dit->video_patch = cfg->video_patch;
+    dit->audio_channels = cfg->audio_channels;
+    dit->video_total = video_total;
+    dit->audio_total = audio_total;
+    dit->video_conditions = video_conditions;
+    dit->audio_conditions = audio_conditions;
+    dit->video_targets = video_targets;
+    dit->audio_targets = audio_targets;
+    dit->video_target_start = video_start;
+    dit->audio_target_start = audio_start;
+    dit->sampler = 1;
+    dit->video_sigmas = (float *)malloc((steps + 1) * sizeof(float));
+    dit->audio_sigmas = (float *)malloc((steps + 1) * sizeof(float));
+    dit->segments = (h3hip_segment *)malloc(
+        (layout->segment_count ? layout->segment_count : 1) *
+        sizeof(h3hip_segment));
+    dit->step_maps = (h3_gpu_tensor **)calloc(steps, sizeof(void *));
+    dit->final_video_maps = (h3_gpu_tensor **)calloc(steps, sizeof(void *));
+    dit->final_audio_maps = (h3_gpu_tensor **)calloc(steps, sizeof(void *));
+    uint32_t *rows = (uint32_t *)malloc((size_t)c->rows * sizeof(uint32_t));
+    uint32_t *video = (uint32_t *)malloc(
+        (video_targets ? video_targets : 1) * sizeof(uint32_t));
+    uint32_t *audio = (uint32_t *)malloc(
+        (audio_targets ? audio_targets : 1) * sizeof(uint32_t));
+    ok = dit->video_sigmas && dit->audio_sigmas && dit->segments &&
+         dit->step_maps && dit->final_video_maps && dit->final_audio_maps &&
+         rows && video && audio;
+    if (ok) {
+        memcpy(dit->video_sigmas, cfg->video_sigmas,
+               (steps + 1) * sizeof(float));
+        memcpy(dit->audio_sigmas, cfg->audio_sigmas,
+               (steps + 1) * sizeof(float));
+        memcpy(dit->segments, layout->segments,
+               layout->segment_count * sizeof(h3hip_segment));
+        dit->segment_count = layout->segment_count;
+    }
+    /* per-step maps (reference prepare_maps, h3_dit.c:1134-1200) */
+    for (int step = 0; step < steps && ok; step++) {
+        ok = h3hip_row_map(layout, video_time[step], audio_time[step],
+                           visual_time[step], audio_cond_time[step], NULL,
+                           text_rows, rows, c->rows);
+        if (!ok) {
+            dit_fail(dit, "cannot build the row map of step %d", step);
+            break;
+        }
+        for (uint32_t r = 0; r < video_targets; r++) video[r] = video_time[step];
+        for (uint32_t r = 0; r < audio_targets; r++) audio[r] = audio_time[step];
+        dit->step_maps[step] = h3_gpu_tensor_from_u32(dit->gpu, rows, c->rows);
+        dit->final_video_maps[step] =
+            h3_gpu_tensor_from_u32(dit->gpu, video, video_targets);
+        dit->final_audio_maps[step] =
+            h3_gpu_tensor_from_u32(dit->gpu, audio, audio_targets);
+        ok = dit->step_maps[step] && dit->final_video_maps[step] &&
+             dit->final_audio_maps[step];
+        if (!ok) dit_fail(dit, "row map upload: %s", h3_gpu_error(dit->gpu));
+    }
+    free(rows); free(video); free(audio);
+    free(video_time); free(audio_time); free(visual_time);
+    free(audio_cond_time);
+    if (!ok) {
+        if (!dit->error[0]) dit_fail(dit, "out of memory");
+        sampler_free(dit);
+        dit->sampler = 0;
+        return 0;
+    }
+    const size_t d = c->hidden, vp = cfg->video_patch;
+    const size_t ac = cfg->audio_channels;
+    h3_gpu *gpu = dit->gpu;
+    int alloc = 1;
+#define F32T(n) (h3_gpu_tensor_new_f32(gpu, (n)))
+    dit->video_input = F32T((size_t)video_total * vp + 1);
+    dit->audio_input = F32T((size_t)audio_total * ac + 1);
+    dit->video_patch_w = F32T(d * vp);
+    dit->video_patch_b = F32T(d);
+    dit->audio_patch_w = F32T(d * ac);
+    dit->audio_patch_b = F32T(d);
+    dit->video_inverse = F32T((size_t)video_targets + 1);
+    dit->audio_inverse = F32T((size_t)audio_targets + 1);
+#undef F32T
+    dit->refined_text = bf16(dit, (size_t)text_rows * d + 1, &alloc);
+    dit->final_norm = bf16(dit, d, &alloc);
+    dit->final_mod = bf16(dit, (size_t)time_rows * 2 * d, &alloc);
+    dit->final_video_w = bf16(dit, vp * d, &alloc);
+    dit->final_video_b = bf16(dit, vp, &alloc);
+    dit->final_audio_w = bf16(dit, ac * d, &alloc);
+    dit->final_audio_b = bf16(dit, ac, &alloc);
+    dit->video_velocity = bf16(dit, (size_t)video_targets * vp + 1, &alloc);
+    dit->audio_velocity = bf16(dit, (size_t)audio_targets * ac + 1, &alloc);
+    dit->video_previous = bf16(dit, (size_t)video_targets * vp + 1, &alloc);
+    dit->audio_previous = bf16(dit, (size_t)audio_targets * ac + 1, &alloc);
+    alloc = alloc && dit->video_input && dit->audio_input &&
+            dit->video_patch_w && dit->video_patch_b && dit->audio_patch_w &&
+            dit->audio_patch_b && dit->video_inverse && dit->audio_inverse;
+    if (!alloc) {
+        dit_fail(dit, "cannot allocate sampler tensors: %s",
+                 h3_gpu_error(gpu));
+        sampler_free(dit);
+        dit->sampler = 0;
+        return 0;
+    }
+    dit->default_row_map = dit->row_map;
+    return 1;
+}
+
+static int fill_f32(h3hip_dit *dit, h3_gpu_tensor *t, uint64_t *seed,
+                    float mean, float std) {
+    return h3_gpu_fill_normal_f32(dit->gpu, t, 0, h3_gpu_tensor_elements(t),
+                                  (*seed)++, mean, std);
+}
+
+int h3hip_dit_sampler_init_random(h3hip_dit *dit, uint64_t seed,
+                                  float weight_std, float mod_std) {
+    if (!dit || !dit->sampler) return dit ? dit_fail(dit, "no sampler") : 0;
+    h3_gpu *gpu = dit->gpu;
+    uint64_t s = seed * 7919ull + 101;
+    if (!dit_op(dit, h3_gpu_begin(gpu), "begin sampler init")) return 0;
+    int ok = fill_f32(dit, dit->video_patch_w, &s, 0.0f, weight_std) &&
+             fill_f32(dit, dit->video_patch_b, &s, 0.0f, 0.02f) &&
+             fill_f32(dit, dit->audio_patch_w, &s, 0.0f, weight_std) &&
+             fill_f32(dit, dit->audio_patch_b, &s, 0.0f, 0.02f) &&
+             fill(dit, dit->refined_text, &s, 0.0f, 1.0f) &&
+             fill(dit, dit->final_norm, &s, 1.0f, 0.02f) &&
+             fill(dit, dit->final_mod, &s, 0.0f, mod_std) &&
+             fill(dit, dit->final_video_w, &s, 0.0f, weight_std) &&
+             fill(dit, dit->final_video_b, &s, 0.0f, 0.02f) &&
+             fill(dit, dit->final_audio_w, &s, 0.0f, weight_std) &&
+             fill(dit, dit->final_audio_b, &s, 0.0f, 0.02f) &&
+             fill_f32(dit, dit->video_input, &s, 0.0f, 1.0f) &&
+             fill_f32(dit, dit->audio_input, &s, 0.0f, 1.0f);
+    if (!ok) {
+        dit_fail(dit, "sampler init: %s", h3_gpu_error(gpu));
+        (void)h3_gpu_submit(gpu);
+        return 0;
+    }
+    return dit_op(dit, h3_gpu_submit(gpu), "submit sampler init");
+}
+
+int h3hip_dit_sampler_write_latents(h3hip_dit *dit, const float *video,
+                                    const float *audio) {
+    if (!dit || !dit->sampler) return dit ? dit_fail(dit, "no sampler") : 0;
+    int ok = (!video || h3_gpu_tensor_write_f32_range(
+                            dit->video_input, 0, video,
+                            (size_t)dit->video_total * dit->video_patch)) &&
+             (!audio || h3_gpu_tensor_write_f32_range(
+                            dit->audio_input, 0, audio,
+                            (size_t)dit->audio_total * dit->audio_channels));
+    return ok ? 1 : dit_fail(dit, "latent upload: %s", h3_gpu_error(dit->gpu));
+}
+
+int h3hip_dit_sampler_read_latents(h3hip_dit *dit, float *video,
+                                   float *audio) {
+    if (!dit || !dit->sampler) return dit ? dit_fail(dit, "no sampler") : 0;
+    int ok = (!video || h3_gpu_tensor_read_f32_range(
+                            dit->video_input, 0, video,
+                            (size_t)dit->video_total * dit->video_patch)) &&
+             (!audio || h3_gpu_tensor_read_f32_range(
+                            dit->audio_input, 0, audio,
+                            (size_t)dit->audio_total * dit->audio_channels));
+    return ok ? 1 : dit_fail(dit, "latent readback: %s",
+                             h3_gpu_error(dit->gpu));
+}
+
+/* Pack, blocks, final heads (reference encode_forward, h3_dit.c:2182-2528,
+ * fused patch/pack and fused final head path). */
+int h3hip_dit_forward_step(h3hip_dit *dit, int step) {
+    if (!dit || !dit->sampler) return dit ? dit_fail(dit, "no sampler") : 0;
+    if (step < 0 || step >= dit->steps)
+        return dit_fail(dit, "step %d outside %d steps", step, dit->steps);
+    const h3hip_dit_config *c = &dit->config;
+    h3_gpu *gpu = dit->gpu;
+    const size_t d = c->hidden;
+    size_t video_offset = 0, audio_offset = 0, text_offset = 0;
+    dit->op_mask = H3HIP_OPS_ALL;
+    for (size_t i = 0; i < dit->segment_count; i++) {
+        const h3hip_segment *seg = &dit->segments[i];
+        const uint32_t n = (uint32_t)(seg->stop - seg->start);
+        const size_t destination = seg->start * d;
+        int ok;
+        if (seg->kind == H3HIP_SEG_TEXT) {
+            ok = dit_op(dit, h3_gpu_copy_bf16(gpu, dit->hidden, destination,
+                                              dit->refined_text,
+                                              text_offset * d, (size_t)n * d),
+                        "pack refined text");
+            text_offset += n;
+        } else if (is_video_kind(seg->kind)) {
+            ok = dit_op(dit, h3_gpu_patch_linear_bf16_offset(
+                                 gpu, dit->hidden, destination,
+                                 dit->video_input,
+                                 video_offset * dit->video_patch,
+                                 dit->video_patch_w, dit->video_patch_b, n,
+                                 dit->video_patch, c->hidden),
+                        "project packed video source");
+            video_offset += n;
+        } else {
+            ok = dit_op(dit, h3_gpu_patch_linear_bf16_offset(
+                                 gpu, dit->hidden, destination,
+                                 dit->audio_input,
+                                 audio_offset * dit->audio_channels,
+                                 dit->audio_patch_w, dit->audio_patch_b, n,
+                                 dit->audio_channels, c->hidden),
+                        "project packed audio source");
+            audio_offset += n;
+        }
+        if (!ok) return 0;
+    }
+    dit->row_map = dit->step_maps[step];
+    int ok = h3hip_dit_run_blocks(dit, 0, c->blocks);
+    dit->row_map = dit->default_row_map;
+    if (!ok) return 0;
+    return dit_op(dit, h3_gpu_adaln_linear_bf16(
+                           gpu, dit->audio_velocity, dit->audio_inverse,
+                           dit->hidden, (size_t)dit->audio_target_start * d,
+                           dit->final_norm, dit->final_mod,
+                           dit->final_audio_maps[step], dit->final_audio_w,
+                           dit->final_audio_b, dit->audio_targets, c->hidden,
+                           dit->audio_channels, 2, 0, 1, c->epsilon),
+                  "final audio adaLN + head") &&
+           dit_op(dit, h3_gpu_adaln_linear_bf16(
+                           gpu, dit->video_velocity, dit->video_inverse,
+                           dit->hidden, (size_t)dit->video_target_start * d,
+                           dit->final_norm, dit->final_mod,
+                           dit->final_video_maps[step], dit->final_video_w,
+                           dit->final_video_b, dit->video_targets, c->hidden,
+                           dit->video_patch, 2, 0, 1, c->epsilon),
+                  "final video adaLN + head");
+}
+
+/* Euler loop with velocity reuse (reference denoise_euler_gpu,
+ * h3_dit.c:2745-2917, the bounded one-evaluation command window). */
+int h3hip_dit_denoise(h3hip_dit *dit) {
+    if (!dit || !dit->sampler) return dit ? dit_fail(dit, "no sampler") : 0;
+    h3_gpu *gpu = dit->gpu;
+    const int steps = dit->steps;
+    uint8_t *selected = (uint8_t *)calloc(steps, 1);
+    if (!selected) return dit_fail(dit, "out of memory");
+    if (h3hip_reuse_schedule(steps, dit->reuse_interval, selected, steps) < 0) {
+        free(selected);
+        return dit_fail(dit, "invalid reuse schedule");
+    }
+    const uint32_t video_count = dit->video_targets * dit->video_patch;
+    const uint32_t audio_count = dit->audio_targets * dit->audio_channels;
+    const size_t video_offset = (size_t)dit->video_conditions * dit->video_patch;
+    const size_t audio_offset =
+        (size_t)dit->audio_conditions * dit->audio_channels;
+    int last = -1, previous = -1, evaluations = 0, ok = 1, open = 0;
+    for (int step = 0; step < steps && ok; step++) {
+        if (!open) {
+            ok = dit_op(dit, h3_gpu_begin(gpu), "begin Euler chain");
+            open = ok;
+            if (!ok) break;
+        }
+        const int evaluate = selected[step];
+        if (evaluate) {
+            if (last >= 0 && dit->reuse_interval > 1) {
+                ok = dit_op(dit, h3_gpu_copy_bf16(gpu, dit->video_previous, 0,
+                                                  dit->video_velocity, 0,
+                                                  video_count),
+                            "cache previous video velocity") &&
+                     dit_op(dit, h3_gpu_copy_bf16(gpu, dit->audio_previous, 0,
+                                                  dit->audio_velocity, 0,
+                                                  audio_count),
+                            "cache previous audio velocity");
+                if (ok) previous = last;
+            }
+            if (ok) ok = h3hip_dit_forward_step(dit, step);
+            if (ok) {
+                last = step;
+                evaluations++;
+            }
+        }
+        if (!ok) break;
+        const int have = previous >= 0;
+        const float video_ratio = evaluate ? 0.0f : h3hip_extrapolation_ratio(
+            dit->video_sigmas[step], dit->video_sigmas[last],
+            have ? dit->video_sigmas[previous] : 0.0f, have);
+        const float audio_ratio = evaluate ? 0.0f : h3hip_extrapolation_ratio(
+            dit->audio_sigmas[step], dit->audio_sigmas[last],
+            have ? dit->audio_sigmas[previous] : 0.0f, have);
+        ok = dit_op(dit, h3_gpu_euler_bf16(
+                         gpu, dit->video_input, video_offset,
+                         dit->video_velocity,
+                         have ? dit->video_previous : dit->video_velocity,
+                         video_count,
+                         dit->video_sigmas[step] - dit->video_sigmas[step + 1],
+                         video_ratio),
+                    "video Euler step") &&
+             dit_op(dit, h3_gpu_euler_bf16(
+                         gpu, dit->audio_input, audio_offset,
+                         dit->audio_velocity,
+                         have ? dit->audio_previous : dit->audio_velocity,
+                         audio_count,
+                         dit->audio_sigmas[step] - dit->audio_sigmas[step + 1],
+                         audio_ratio),
+                    "audio Euler step");
+        if (ok && evaluate) {
+            ok = dit_op(dit, h3_gpu_submit(gpu), "submit Euler window");
+            open = 0;
+        }
+    }
+    if (open) {
+        if (ok) ok = dit_op(dit, h3_gpu_submit(gpu), "submit Euler denoise");
+        else (void)h3_gpu_submit(gpu);
+    }
+    free(selected);
+    return ok ? evaluations : 0;
 }

@@ -18,6 +18,7 @@
 
 #include "../../include/h3_gpu.h"
 #include "../../include/h3_hip.h"
+#include "h3hip_host.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -68,6 +69,13 @@ int h3hip_dit_set_row_map(h3hip_dit *dit, const uint32_t *row_map);
  *              "cq_norm" "ck_norm" "co" "co_bias" "modulation"
  *   shared (block ignored): "hidden" "row_map" "rope_cos" "rope_sin"
  *              "context"
+ *   sampler (block ignored): "video_input" "audio_input" "video_patch_w"
+ *              "video_patch_b" "audio_patch_w" "audio_patch_b"
+ *              "refined_text" "final_norm" "final_modulation"
+ *              "final_video_w" "final_video_b" "final_audio_w"
+ *              "final_audio_b" "video_velocity" "audio_velocity"
+ *   per step (block = step): "step_row_map" "final_video_map"
+ *              "final_audio_map"
  * Returns NULL for a name the family does not use. */
 h3_gpu_tensor *h3hip_dit_tensor(h3hip_dit *dit, const char *name,
                                 uint32_t block);
@@ -102,6 +110,54 @@ double h3hip_dit_block_flops(const h3hip_dit_config *config);
 /* FLOPs of the GEMMs alone and of the attention alone. */
 double h3hip_dit_block_gemm_flops(const h3hip_dit_config *config);
 double h3hip_dit_block_attention_flops(const h3hip_dit_config *config);
+
+/* ------------------------------------------------------------------
+ * H3 sampler: the step either side of the blocks and the Euler loop
+ * (reference h3_dit.c encode_forward :2182-2528, denoise_euler_gpu
+ * :2745-2917, prepare_maps :1134-1200).
+ *
+ * The packed sequence follows `layout` (config.rows == layout->seq_len):
+ * text segments are copied from the refined text rows, video-kind segments
+ * (condition, reference image, video) are projected from the F32 video
+ * latent rows in layout order, audio-kind segments (reference audio, audio)
+ * from the audio latent rows.  The layout holds one video and one audio
+ * target segment, each after its modality's condition segments.  The
+ * modulation of every block has one row per time row of the schedule
+ * (config.time_rows must equal h3hip_time_rows() for these sigmas); the
+ * final adaLN modulation is [time_rows][2][hidden].
+ * ------------------------------------------------------------------ */
+typedef struct {
+    const h3hip_layout *layout;
+    int steps;
+    const float *video_sigmas;  /* steps + 1 */
+    const float *audio_sigmas;  /* steps + 1 */
+    int reuse_interval;         /* 1 = every step evaluated */
+    uint32_t video_patch;       /* 96 */
+    uint32_t audio_channels;    /* 32 */
+} h3hip_sampler_config;
+
+/* Allocate the sampler tensors and upload the per-step row maps. */
+int h3hip_dit_sampler_create(h3hip_dit *dit, const h3hip_sampler_config *cfg);
+/* Seeded init of the patch projections (F32), final norm, final heads,
+ * final modulation and refined text rows, like h3hip_dit_init_random. */
+int h3hip_dit_sampler_init_random(h3hip_dit *dit, uint64_t seed,
+                                  float weight_std, float mod_std);
+/* Write / read the F32 latent rows: video [video rows][video_patch],
+ * audio [audio rows][audio_channels], condition rows first. */
+int h3hip_dit_sampler_write_latents(h3hip_dit *dit, const float *video,
+                                    const float *audio);
+int h3hip_dit_sampler_read_latents(h3hip_dit *dit, float *video,
+                                   float *audio);
+/* One forward at `step` inside an open batch: pack the sequence, run all
+ * blocks, final adaLN + heads into the bf16 velocity tensors. */
+int h3hip_dit_forward_step(h3hip_dit *dit, int step);
+/* The whole Euler denoise with velocity reuse; opens and submits its own
+ * batches. Returns the number of forwards evaluated, 0 on failure. */
+int h3hip_dit_denoise(h3hip_dit *dit);
+/* Rows of each latent array: video / audio totals and their targets. */
+void h3hip_dit_sampler_rows(const h3hip_dit *dit, uint32_t *video_rows,
+                            uint32_t *audio_rows, uint32_t *video_targets,
+                            uint32_t *audio_targets);
 
 const char *h3hip_dit_error(const h3hip_dit *dit);
 

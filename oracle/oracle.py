@@ -288,6 +288,109 @@ def h3_blocks(hidden, blocks, row_map, cos, sin, rows, hidden_dim, heads, ffn,
     return x
 
 
+def reuse_schedule(steps, interval):
+    """Evaluated steps under velocity reuse (h3_dit.c:2672-2687)."""
+    return [interval == 1 or s == 0 or s == steps - 1 or s % interval == 0
+            for s in range(steps)]
+
+
+def extrapolation_ratio(current, last, previous, have_previous):
+    """Clamped linear velocity extrapolation ratio (h3_dit.c:2644-2655),
+    evaluated in F32 like the reference."""
+    if not have_previous:
+        return np.float32(0.0)
+    den = np.float32(last) - np.float32(previous)
+    r = ((np.float32(current) - np.float32(last)) / den
+         if den != 0 else np.float32(0.0))
+    return np.float32(min(max(r, -2.0), 2.0))
+
+
+def h3_forward_step(m, step):
+    """One sampler forward (h3_dit.c:2182-2528, fused patch/pack and fused
+    final-head path): pack text / patch-projected latent rows into the
+    sequence in layout order, run the blocks with the step's row map, then
+    the final adaLN + heads of the audio and video targets.  `m` is a dict
+    holding the model (see tests/test_sampler_gpu.py); returns (video,
+    audio) velocities as bf16 bits."""
+    d, vp, ac = m["hidden"], m["video_patch"], m["audio_channels"]
+    hidden = np.zeros(m["rows"] * d, np.uint16)
+    vo = ao = to = 0
+    for start, stop, kind in m["segments"]:
+        n = stop - start
+        if kind == 0:
+            hidden[start * d:stop * d] = m["refined_text"][to * d:(to + n) * d]
+            to += n
+        elif kind in (1, 2, 5):
+            hidden[start * d:stop * d] = patch_linear(
+                m["video_input"][vo * vp:(vo + n) * vp], m["video_patch_w"],
+                m["video_patch_b"], n, vp, d)
+            vo += n
+        else:
+            hidden[start * d:stop * d] = patch_linear(
+                m["audio_input"][ao * ac:(ao + n) * ac], m["audio_patch_w"],
+                m["audio_patch_b"], n, ac, d)
+            ao += n
+    x = h3_blocks(hidden, m["blocks"], m["step_maps"][step], m["cos"],
+                  m["sin"], m["rows"], d, m["heads"], m["ffn"],
+                  eps=m["eps"])
+    a0, na = m["audio_target_start"], m["audio_targets"]
+    v0, nv = m["video_target_start"], m["video_targets"]
+    audio, _ = adaln_linear(x[a0 * d:(a0 + na) * d], m["final_norm"],
+                            m["final_modulation"],
+                            m["final_audio_maps"][step], m["final_audio_w"],
+                            m["final_audio_b"], na, d, ac, 2, 0, 1, m["eps"])
+    video, _ = adaln_linear(x[v0 * d:(v0 + nv) * d], m["final_norm"],
+                            m["final_modulation"],
+                            m["final_video_maps"][step], m["final_video_w"],
+                            m["final_video_b"], nv, d, vp, 2, 0, 1, m["eps"])
+    return video, audio
+
+
+def h3_denoise(m, video_sigmas, audio_sigmas, reuse_interval):
+    """The GPU Euler loop with velocity reuse (h3_dit.c:2745-2917): cache
+    the previous velocity before each fresh evaluation, extrapolate on the
+    skipped steps, x += (sigma_i - sigma_i+1) (v + r (v - v_prev)).
+    Returns the updated (video, audio) F32 latent rows and the number of
+    evaluations."""
+    steps = len(video_sigmas) - 1
+    vp, ac = m["video_patch"], m["audio_channels"]
+    video = np.array(m["video_input"], np.float32)
+    audio = np.array(m["audio_input"], np.float32)
+    voff = m["video_conditions"] * vp
+    aoff = m["audio_conditions"] * ac
+    sel = reuse_schedule(steps, reuse_interval)
+    last = previous = -1
+    vv = av = vprev = aprev = None
+    evaluations = 0
+    for step in range(steps):
+        if sel[step]:
+            if last >= 0 and reuse_interval > 1:
+                vprev, aprev = vv.copy(), av.copy()
+                previous = last
+            mm = dict(m, video_input=video, audio_input=audio)
+            vv, av = h3_forward_step(mm, step)
+            last = step
+            evaluations += 1
+        have = previous >= 0
+        if sel[step]:
+            vr = ar = np.float32(0.0)
+        else:
+            vr = extrapolation_ratio(video_sigmas[step], video_sigmas[last],
+                                     video_sigmas[previous] if have else 0.0,
+                                     have)
+            ar = extrapolation_ratio(audio_sigmas[step], audio_sigmas[last],
+                                     audio_sigmas[previous] if have else 0.0,
+                                     have)
+        vdt = np.float32(video_sigmas[step]) - np.float32(video_sigmas[step + 1])
+        adt = np.float32(audio_sigmas[step]) - np.float32(audio_sigmas[step + 1])
+        nv, na = vv.size, av.size
+        video[voff:voff + nv] = euler(video[voff:voff + nv], vv,
+                                      vprev if have else vv, vdt, vr)
+        audio[aoff:aoff + na] = euler(audio[aoff:aoff + na], av,
+                                      aprev if have else av, adt, ar)
+    return video, audio, evaluations
+
+
 def wan_block(hidden, context, w, row_map, cos, sin, rows, text_rows, d,
               heads, ffn, hd=128, rope_half=48, eps=1e-6):
     """One Wan-style block in the op order of the HIP driver
