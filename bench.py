@@ -155,6 +155,11 @@ def h3_measure(gpu, blocks, reps):
         hdit.set_rope(hc, hs)
         hdit.sampler_create(lay, v_sig, a_sig, reuse_interval=2)
         hdit.sampler_init_random(seed=2, weight_std=0.02, mod_std=0.1)
+        # modulation of all 39 time rows from the random-init time MLP and
+        # adaLN projections (reference h3_dit_schedule.c:78-337)
+        t0 = time.perf_counter()
+        hdit.schedule_precompute(seed=3, weight_std=0.02)
+        precompute_s = time.perf_counter() - t0
         # forward alone, on the step-0 modulation rows
         hdit.gpu.begin()
         if not L.h3hip_dit_forward_step(hdit.h, 0):
@@ -176,7 +181,9 @@ def h3_measure(gpu, blocks, reps):
                          "(2378 rows), 50 blocks",
                "steps": steps, "fresh_forwards": int(evaluations),
                "seconds": round(seconds, 3),
-               "s_per_fresh_forward": round(seconds / evaluations, 4)}
+               "s_per_fresh_forward": round(seconds / evaluations, 4),
+               "schedule_precompute_s": round(precompute_s, 3),
+               "time_rows": int(time_rows)}
     finally:
         hdit.close()
         L.h3hip_layout_free(C.byref(lay))

@@ -350,6 +350,82 @@ hk_gemm_mfma(hk_gemm_args g) {
     }
 }
 
+/* Skinny GEMM for M <= 64 rows (the per-block modulation projections:
+ * time rows x 2688 against 96768 x 2688 weights).  Bound by streaming W
+ * from HBM once, so no LDS: each workgroup owns a 64 (M) x 64 (N) output
+ * tile, its four waves a 32 x 32 quarter, and every wave reads its MFMA
+ * fragments straight from global memory (16 bytes per lane, rows past M or
+ * N read as zeros through the buffer bound), one 64-wide k-step ahead of
+ * the MFMAs.  X is tiny and stays in L2; each W row is read by the two
+ * waves that share its column half, the second read hitting L2. */
+__global__ void __launch_bounds__(256)
+hk_gemm_skinny(const uint16_t *x, const uint16_t *w, const uint16_t *bias,
+               uint16_t *c, uint32_t m, uint32_t n, uint32_t k,
+               uint32_t x_bytes, uint32_t w_bytes) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t wm = wave & 1u, wn = wave >> 1;
+    const uint32_t row = lane & 31u, half = lane >> 5;
+    const uint32_t m0 = blockIdx.y * 64u + wm * 32u;
+    const uint32_t n0 = blockIdx.x * 64u + wn * 32u;
+    const __amdgpu_buffer_rsrc_t xr = hk_rsrc(x, x_bytes);
+    const __amdgpu_buffer_rsrc_t wr = hk_rsrc(w, w_bytes);
+    const uint32_t xo = m0 + row < m ? ((m0 + row) * k + half * 8u) * 2u
+                                     : 0xfffffff0u;
+    const uint32_t wo = n0 + row < n ? ((n0 + row) * k + half * 8u) * 2u
+                                     : 0xfffffff0u;
+    auto load = [&](hk_v4i (&fx)[4], hk_v4i (&fw)[4], uint32_t k0) {
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const uint32_t kb = (k0 + s * 16u) * 2u;
+            fx[s] = __builtin_amdgcn_raw_buffer_load_b128(
+                xr, xo == 0xfffffff0u ? xo : xo + kb, 0, 0);
+            fw[s] = __builtin_amdgcn_raw_buffer_load_b128(
+                wr, wo == 0xfffffff0u ? wo : wo + kb, 0, 0);
+        }
+    };
+    hk_f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+    hk_v4i fx[2][4], fw[2][4];
+    load(fx[0], fw[0], 0);
+    const uint32_t steps = k / 64u;
+    for (uint32_t s = 0; s < steps; s += 2) {
+        if (s + 1 < steps) load(fx[1], fw[1], (s + 1) * 64u);
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(hk_bf16x8, fw[0][q]),
+                __builtin_bit_cast(hk_bf16x8, fx[0][q]), acc, 0, 0, 0);
+        if (s + 1 >= steps) break;
+        if (s + 2 < steps) load(fx[0], fw[0], (s + 2) * 64u);
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(hk_bf16x8, fw[1][q]),
+                __builtin_bit_cast(hk_bf16x8, fx[1][q]), acc, 0, 0, 0);
+    }
+    /* acc[r] = C[m0 + row][n0 + (r/4)*8 + half*4 + r%4] */
+    const uint32_t mm = m0 + row;
+    if (mm >= m) return;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const uint32_t col = n0 + q * 8u + half * 4u;
+        if (col >= n) continue;
+        float out[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) out[e] = acc[q * 4 + e];
+        if (bias) {
+            uint2 b = *(const uint2 *)(bias + col);
+            out[0] += hk_bf2f(b.x & 0xffffu);
+            out[1] += hk_bf2f(b.x >> 16);
+            out[2] += hk_bf2f(b.y & 0xffffu);
+            out[3] += hk_bf2f(b.y >> 16);
+        }
+        *(uint2 *)(c + (size_t)mm * n + col) =
+            uint2{hk_pack2(out[0], out[1]), hk_pack2(out[2], out[3])};
+    }
+}
+
 /* Sequential-k reference GEMM (any shape).  For SwiGLU it writes the fused
  * [M, 2N] bf16 projection into `c` (caller runs the activation). */
 __global__ void hk_gemm_reference(const uint16_t *x, const uint16_t *w,
@@ -392,6 +468,12 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
                       (epilogue != HK_EPI_SWIGLU || n % 64 == 0) &&
                       ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 &&
                       ((uintptr_t)c & 7) == 0 && ((uintptr_t)bias & 7) == 0;
+    if (mfma && m <= 64 && epilogue == HK_EPI_STORE) {
+        hipLaunchKernelGGL(hk_gemm_skinny, dim3((n + 63) / 64, (m + 63) / 64),
+                           dim3(256), 0, gpu->stream, x, w, bias, c, m, n, k,
+                           (uint32_t)x_bytes, (uint32_t)w_bytes);
+        return 1;
+    }
     if (mfma) {
         if (!hk_gemm_lds_ready) {
             (void)hipFuncSetAttribute(

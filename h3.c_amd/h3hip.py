@@ -189,6 +189,7 @@ def lib():
         "h3hip_dit_sampler_read_latents": (_I, [_P, _P, _P]),
         "h3hip_dit_forward_step": (_I, [_P, _I]),
         "h3hip_dit_denoise": (_I, [_P]),
+        "h3hip_dit_schedule_precompute": (_I, [_P, C.c_uint64, _F]),
         "h3hip_dit_sampler_rows": (None, [_P, C.POINTER(_U32),
                                           C.POINTER(_U32), C.POINTER(_U32),
                                           C.POINTER(_U32)]),
@@ -485,6 +486,11 @@ class Dit:
             raise RuntimeError(msg)
         if submit:
             self.gpu.submit()
+
+    def schedule_precompute(self, seed, weight_std=0.02):
+        if not self.gpu.L.h3hip_dit_schedule_precompute(self.h, seed,
+                                                        weight_std):
+            raise RuntimeError(self.error())
 
     def denoise(self):
         n = self.gpu.L.h3hip_dit_denoise(self.h)

@@ -51,6 +51,7 @@ struct h3hip_dit {
     h3_gpu_tensor *video_inverse, *audio_inverse;
     h3_gpu_tensor **step_maps, **final_video_maps, **final_audio_maps;
     h3_gpu_tensor *default_row_map;
+    h3_gpu_tensor *time_in_w, *time_in_b, *time_out_w, *time_out_b;
     char error[512];
 };
 
@@ -258,7 +259,10 @@ h3_gpu_tensor *h3hip_dit_tensor(h3hip_dit *dit, const char *name,
             {"final_audio_w", dit->final_audio_w},
             {"final_audio_b", dit->final_audio_b},
             {"video_velocity", dit->video_velocity},
-            {"audio_velocity", dit->audio_velocity}};
+            {"audio_velocity", dit->audio_velocity},
+            {"time_in_w", dit->time_in_w}, {"time_in_b", dit->time_in_b},
+            {"time_out_w", dit->time_out_w},
+            {"time_out_b", dit->time_out_b}};
         for (size_t i = 0; i < sizeof(shared) / sizeof(*shared); i++)
             if (!strcmp(name, shared[i].name)) return shared[i].tensor;
         if ((int)block < dit->steps) {
@@ -591,7 +595,8 @@ static void sampler_free(h3hip_dit *dit) {
         dit->final_video_w, dit->final_video_b, dit->final_audio_w,
         dit->final_audio_b, dit->video_velocity, dit->audio_velocity,
         dit->video_previous, dit->audio_previous, dit->video_inverse,
-        dit->audio_inverse};
+        dit->audio_inverse, dit->time_in_w, dit->time_in_b, dit->time_out_w,
+        dit->time_out_b};
     for (size_t i = 0; i < sizeof(owned) / sizeof(*owned); i++)
         h3_gpu_tensor_free(owned[i]);
     free_maps(dit->step_maps, dit->steps);
@@ -1005,4 +1010,118 @@ int h3hip_dit_denoise(h3hip_dit *dit) {
     }
     free(selected);
     return ok ? evaluations : 0;
+}
+
+/* ------------------------------------------------- modulation schedule */
+
+enum { TIME_INPUT = 256 };
+
+int h3hip_dit_schedule_precompute(h3hip_dit *dit, uint64_t seed,
+                                  float weight_std) {
+    if (!dit || !dit->sampler)
+        return dit ? dit_fail(dit, "the schedule needs the sampler") : 0;
+    const h3hip_dit_config *c = &dit->config;
+    const uint32_t d = c->hidden, th = d, td = d / 2;
+    if (d % 2 || td % 64)
+        return dit_fail(dit, "hidden %u has no 64-aligned half", d);
+    /* time rows and their t = 1 - sigma (h3_dit_schedule.c:78-161) */
+    const int steps = dit->steps;
+    int visual = 0, audio_cond = 0;
+    for (size_t i = 0; i < dit->segment_count; i++) {
+        const int kind = dit->segments[i].kind;
+        if (kind == H3HIP_SEG_COND || kind == H3HIP_SEG_REF_IMAGE) visual = 1;
+        if (kind == H3HIP_SEG_REF_AUDIO) audio_cond = 1;
+    }
+    uint32_t *rows4 = (uint32_t *)calloc(4 * (size_t)steps, sizeof(uint32_t));
+    float *times = (float *)calloc(c->time_rows, sizeof(float));
+    float *features =
+        (float *)malloc((size_t)c->time_rows * TIME_INPUT * sizeof(float));
+    if (!rows4 || !times || !features) {
+        free(rows4); free(times); free(features);
+        return dit_fail(dit, "out of memory");
+    }
+    uint32_t n = h3hip_time_rows(steps, dit->video_sigmas, dit->audio_sigmas,
+                                 visual, audio_cond, rows4, rows4 + steps,
+                                 rows4 + 2 * steps, rows4 + 3 * steps, times);
+    if (n != c->time_rows) {
+        free(rows4); free(times); free(features);
+        return dit_fail(dit, "schedule has %u time rows, the DiT %u", n,
+                        c->time_rows);
+    }
+    h3hip_timestep_features(times, n, features);
+    free(rows4);
+    free(times);
+
+    h3_gpu *gpu = dit->gpu;
+    if (!dit->time_in_w) {
+        dit->time_in_w = h3_gpu_tensor_new_f32(gpu, (size_t)th * TIME_INPUT);
+        dit->time_in_b = h3_gpu_tensor_new_f32(gpu, th);
+        dit->time_out_w = h3_gpu_tensor_new_f32(gpu, (size_t)td * th);
+        dit->time_out_b = h3_gpu_tensor_new_f32(gpu, td);
+    }
+    const size_t block_out = (size_t)dit->modalities * SLOTS * d;
+    h3_gpu_tensor *feat =
+        h3_gpu_tensor_from_f32(gpu, features, (size_t)n * TIME_INPUT);
+    free(features);
+    h3_gpu_tensor *h1 = h3_gpu_tensor_new_f32(gpu, (size_t)n * th);
+    h3_gpu_tensor *a1 = h3_gpu_tensor_new_f32(gpu, (size_t)n * th);
+    h3_gpu_tensor *o = h3_gpu_tensor_new_f32(gpu, (size_t)n * td);
+    h3_gpu_tensor *ob = h3_gpu_tensor_new_bf16(gpu, (size_t)n * td);
+    h3_gpu_tensor *time = h3_gpu_tensor_new_bf16(gpu, (size_t)n * td);
+    h3_gpu_tensor *pw = h3_gpu_tensor_new_bf16(gpu, block_out * td);
+    h3_gpu_tensor *pb = h3_gpu_tensor_new_bf16(gpu, block_out);
+    h3_gpu_tensor *temps[] = {feat, h1, a1, o, ob, time, pw, pb};
+    int ok = dit->time_in_w && dit->time_in_b && dit->time_out_w &&
+             dit->time_out_b;
+    for (size_t i = 0; i < sizeof(temps) / sizeof(*temps); i++)
+        ok = ok && temps[i];
+    if (!ok) {
+        for (size_t i = 0; i < sizeof(temps) / sizeof(*temps); i++)
+            h3_gpu_tensor_free(temps[i]);
+        return dit_fail(dit, "cannot allocate schedule tensors: %s",
+                        h3_gpu_error(gpu));
+    }
+#define SOP(call, what) (ok = ok && dit_op(dit, (call), (what)))
+    ok = dit_op(dit, h3_gpu_begin(gpu), "begin schedule precompute");
+    SOP(h3_gpu_fill_normal_f32(gpu, dit->time_in_w, 0, (size_t)th * TIME_INPUT,
+                               seed, 0.0f, weight_std), "time MLP init");
+    SOP(h3_gpu_fill_normal_f32(gpu, dit->time_in_b, 0, th, seed + 1, 0.0f,
+                               0.02f), "time MLP init");
+    SOP(h3_gpu_fill_normal_f32(gpu, dit->time_out_w, 0, (size_t)td * th,
+                               seed + 2, 0.0f, weight_std), "time MLP init");
+    SOP(h3_gpu_fill_normal_f32(gpu, dit->time_out_b, 0, td, seed + 3, 0.0f,
+                               0.02f), "time MLP init");
+    /* timestep embedding (h3_dit_schedule.c:163-234) */
+    SOP(h3_gpu_linear_f32(gpu, h1, feat, dit->time_in_w, dit->time_in_b, n,
+                          TIME_INPUT, th), "timestep input projection");
+    SOP(h3_gpu_silu_f32(gpu, a1, h1, n * th), "timestep SiLU");
+    SOP(h3_gpu_linear_f32(gpu, o, a1, dit->time_out_w, dit->time_out_b, n, th,
+                          td), "timestep output projection");
+    SOP(h3_gpu_cast_f32_to_bf16(gpu, ob, o, n * td), "timestep BF16 cast");
+    SOP(h3_gpu_silu_bf16(gpu, time, ob, n * td), "timestep adaLN SiLU");
+    /* per-block adaLN projections (h3_dit_schedule.c:260-301) */
+    for (uint32_t b = 0; b < c->blocks && ok; b++) {
+        SOP(h3_gpu_fill_normal_bf16(gpu, pw, 0, block_out * td,
+                                    seed + 16 + 2ull * b, 0.0f, weight_std),
+            "adaLN projection init");
+        SOP(h3_gpu_fill_normal_bf16(gpu, pb, 0, block_out,
+                                    seed + 17 + 2ull * b, 0.0f, 0.02f),
+            "adaLN projection init");
+        SOP(h3_gpu_linear_bf16(gpu, dit->blocks[b].modulation, time, pw, pb,
+                               n, td, (uint32_t)block_out),
+            "adaLN block projection");
+    }
+    /* final adaLN projection (h3_dit_schedule.c:303-330) */
+    SOP(h3_gpu_fill_normal_bf16(gpu, pw, 0, (size_t)2 * d * td, seed + 8, 0.0f,
+                                weight_std), "final adaLN init");
+    SOP(h3_gpu_fill_normal_bf16(gpu, pb, 0, (size_t)2 * d, seed + 9, 0.0f,
+                                0.02f), "final adaLN init");
+    SOP(h3_gpu_linear_bf16(gpu, dit->final_mod, time, pw, pb, n, td, 2 * d),
+        "final adaLN projection");
+#undef SOP
+    if (ok) ok = dit_op(dit, h3_gpu_submit(gpu), "submit schedule precompute");
+    else (void)h3_gpu_submit(gpu);
+    for (size_t i = 0; i < sizeof(temps) / sizeof(*temps); i++)
+        h3_gpu_tensor_free(temps[i]);
+    return ok;
 }

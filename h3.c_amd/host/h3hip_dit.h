@@ -74,6 +74,8 @@ int h3hip_dit_set_row_map(h3hip_dit *dit, const uint32_t *row_map);
  *              "refined_text" "final_norm" "final_modulation"
  *              "final_video_w" "final_video_b" "final_audio_w"
  *              "final_audio_b" "video_velocity" "audio_velocity"
+ *              "time_in_w" "time_in_b" "time_out_w" "time_out_b" (after
+ *              h3hip_dit_schedule_precompute)
  *   per step (block = step): "step_row_map" "final_video_map"
  *              "final_audio_map"
  * Returns NULL for a name the family does not use. */
@@ -154,6 +156,26 @@ int h3hip_dit_forward_step(h3hip_dit *dit, int step);
 /* The whole Euler denoise with velocity reuse; opens and submits its own
  * batches. Returns the number of forwards evaluated, 0 on failure. */
 int h3hip_dit_denoise(h3hip_dit *dit);
+/* Modulation precompute (reference h3_dit_schedule.c:78-337), after
+ * h3hip_dit_sampler_create: 256-d timestep features of the schedule's
+ * time rows (t = 1 - sigma) -> F32 linear 256 -> hidden, SiLU, F32 linear
+ * hidden -> hidden/2, bf16 cast, bf16 SiLU -> per block the adaLN
+ * projection hidden/2 -> 3 x 6 x hidden (+bias) into that block's
+ * modulation, and the final projection hidden/2 -> 2 x hidden (+bias) into
+ * the final modulation.  Opens and submits its own batch.
+ *
+ * Synthetic weights, generated on the device with h3_gpu_fill_normal_*:
+ * time MLP in/out weights ~ N(0, weight_std^2) with seeds seed, seed + 2,
+ * biases ~ N(0, 0.02^2) with seeds seed + 1, seed + 3 (kept, names
+ * "time_in_w" "time_in_b" "time_out_w" "time_out_b"); the projection of
+ * block b ~ N(0, weight_std^2) with seed seed + 16 + 2b, its bias
+ * ~ N(0, 0.02^2) with seed seed + 17 + 2b; the final projection seeds
+ * seed + 8 and seed + 9.  Like the reference, which loads each block's
+ * projection, uses it once and frees it, the projection weights live in
+ * one buffer that is regenerated per block. */
+int h3hip_dit_schedule_precompute(h3hip_dit *dit, uint64_t seed,
+                                  float weight_std);
+
 /* Rows of each latent array: video / audio totals and their targets. */
 void h3hip_dit_sampler_rows(const h3hip_dit *dit, uint32_t *video_rows,
                             uint32_t *audio_rows, uint32_t *video_targets,

@@ -61,6 +61,20 @@ void orc_bf16_to_f32(const bf16 *in, float *out, size_t n) {
  * h3k_linear_bf16 (h3_cuda_core.cu:358-371), bit for bit.  The loops are
  * blocked (columns x rows) with k innermost-sequential per output so the
  * order of every accumulation is unchanged. */
+/* F32 linear, reference h3_cuda_core.cu:343-356 (h3k_linear_f32: one
+ * output per thread, fmaf over k from the bias). */
+void orc_linear_f32(const float *x, const float *w, const float *bias,
+                    float *out, size_t m, size_t k, size_t n) {
+#pragma omp parallel for schedule(static) collapse(2)
+    for (size_t i = 0; i < m; i++)
+        for (size_t j = 0; j < n; j++) {
+            float sum = bias ? bias[j] : 0.0f;
+            const float *xr = x + i * k, *wr = w + j * k;
+            for (size_t kk = 0; kk < k; kk++) sum = fmaf(xr[kk], wr[kk], sum);
+            out[i * n + j] = sum;
+        }
+}
+
 void orc_linear_bf16(const bf16 *x, const bf16 *w, const bf16 *bias,
                      bf16 *out, size_t m, size_t k, size_t n) {
     enum { JB = 64, IB = 4 };

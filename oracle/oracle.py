@@ -35,6 +35,7 @@ def lib():
         L = C.CDLL(LIB_PATH)
         sig = {
             "orc_linear_bf16": [_P, _P, _P, _P, _SZ, _SZ, _SZ],
+            "orc_linear_f32": [_P, _P, _P, _P, _SZ, _SZ, _SZ],
             "orc_patch_linear": [_P, _P, _P, _P, _P, _SZ, _SZ, _SZ],
             "orc_adaln": [_P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _F],
             "orc_gate": [_P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _SZ],
@@ -95,6 +96,27 @@ def linear(x, w, bias, m, k, n):
                           _p(None if bias is None else _u16(bias)), _p(out),
                           m, k, n)
     return out
+
+
+def linear_f32(x, w, bias, m, k, n):
+    """h3_cuda_core.cu:343-356 (F32, sequential-k fmaf from the bias)."""
+    out = np.empty(m * n, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    lib().orc_linear_f32(_p(x), _p(w), _p(b), _p(out), m, k, n)
+    return out
+
+
+def time_embedding(features, in_w, in_b, out_w, out_b, rows, inp, hid, dim):
+    """The timestep MLP of the schedule precompute (h3_dit_schedule.c:
+    163-234): F32 linear inp -> hid, SiLU (x / (1 + e^-x), :15-20), F32
+    linear hid -> dim, cast to bf16, bf16 SiLU (:23-29).  Returns bf16
+    bits [rows][dim]."""
+    h = linear_f32(features, in_w, in_b, rows, inp, hid)
+    h = (h / (np.float32(1) + np.exp(-h))).astype(np.float32)
+    o = linear_f32(h, out_w, out_b, rows, hid, dim)
+    return silu(bf16(o))
 
 
 def patch_linear(x, w, bias, m, k, n, row_map=None, out_rows=None):

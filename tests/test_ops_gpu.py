@@ -36,6 +36,9 @@ def _mod_setup(rng, rows, width, slots=6, mod_rows=4):
     (300, 5376, 1024, False),   # real K (hidden)
     (257, 1024, 1280, True),    # M just past a tile
     (64, 96, 256, True),        # K % 64 != 0 -> sequential fallback kernel
+    (39, 2688, 4100, True),     # skinny path: time rows x modulation width
+    (64, 128, 68, False),       # skinny path: full 64-row tile, ragged N
+    (65, 192, 256, False),      # one row past the skinny limit
 ])
 def test_linear_bf16(gpu, m, k, n, bias):
     rng = np.random.default_rng(m * 7 + k + n)

@@ -67,6 +67,46 @@ def test_linear_against_float64():
     assert within_one_rounding(got, exact.ravel(), bound.ravel())
 
 
+def test_linear_f32_exact_and_against_float64():
+    """F32 linear: integer inputs are exact (operand order and bias); random
+    inputs stay within the sequential-accumulation bound of float64."""
+    m, k, n = 4, 6, 5
+    x = rng.integers(-4, 5, (m, k)).astype(np.float32)
+    w = rng.integers(-4, 5, (n, k)).astype(np.float32)
+    bias = rng.integers(-3, 4, n).astype(np.float32)
+    got = oracle.linear_f32(x, w, bias, m, k, n).reshape(m, n)
+    np.testing.assert_array_equal(got, x @ w.T + bias)
+    m, k, n = 9, 256, 40
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = (0.1 * rng.standard_normal((n, k))).astype(np.float32)
+    got = oracle.linear_f32(x, w, None, m, k, n).astype(np.float64)
+    exact = x.astype(np.float64) @ w.astype(np.float64).T
+    bound = k * 2.0 ** -24 * (np.abs(x).astype(np.float64) @
+                              np.abs(w).astype(np.float64).T)
+    assert np.all(np.abs(got.reshape(m, n) - exact) <= bound + 1e-30)
+
+
+def test_time_embedding_composition():
+    """The timestep MLP (h3_dit_schedule.c:163-234) against a float64
+    restatement: linear, x * sigmoid(x), linear, then bf16 rounding and the
+    bf16 SiLU; equal within one bf16 rounding of the result."""
+    rows, inp, hid, dim = 3, 16, 12, 8
+    feat = rng.standard_normal(rows * inp).astype(np.float32)
+    w1 = (0.3 * rng.standard_normal(hid * inp)).astype(np.float32)
+    b1 = (0.1 * rng.standard_normal(hid)).astype(np.float32)
+    w2 = (0.3 * rng.standard_normal(dim * hid)).astype(np.float32)
+    b2 = (0.1 * rng.standard_normal(dim)).astype(np.float32)
+    got = f64(oracle.time_embedding(feat, w1, b1, w2, b2, rows, inp, hid,
+                                    dim))
+    h = feat.astype(np.float64).reshape(rows, inp) @ \
+        w1.astype(np.float64).reshape(hid, inp).T + b1
+    h = h / (1 + np.exp(-h))
+    o = h @ w2.astype(np.float64).reshape(dim, hid).T + b2
+    o = f64(b(o.astype(np.float32)))
+    want = (o / (1 + np.exp(-o))).ravel()
+    assert np.all(np.abs(got - want) <= 2.0 ** -7 * np.abs(want) + 1e-6)
+
+
 # ------------------------------------------------------------ row ops
 
 def _adaln64(x, w, mod, rm, rows, width, slots, shift, scale, eps):
