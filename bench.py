@@ -190,6 +190,72 @@ def h3_measure(gpu, blocks, reps):
     return real, den
 
 
+def attention_sweep(gpu):
+    """flash attention alone, bf16, 40 heads x 128, Q/K/V
+    ~ N(0, 1); self-attention at 6144 and 9720 rows, cross-attention of
+    those queries against 512 keys.  HIP events around 10 launches."""
+    import ctypes as C
+    L = gpu.L
+    out = {}
+    scale = 128 ** -0.5
+    for name, q_rows, kv_rows in (("self_6144", 6144, 6144),
+                                  ("self_9720", 9720, 9720),
+                                  ("cross_6144x512", 6144, 512),
+                                  ("cross_9720x512", 9720, 512)):
+        heads = 40
+        tq = gpu.new_bf16(q_rows * heads * 128)
+        tk = gpu.new_bf16(kv_rows * heads * 128)
+        tv = gpu.new_bf16(kv_rows * heads * 128)
+        to = gpu.new_bf16(q_rows * heads * 128)
+        gpu.begin()
+        for i, t in enumerate((tq, tk, tv)):
+            L.h3_gpu_fill_normal_bf16(gpu.h, t, 0,
+                                      L.h3_gpu_tensor_elements(t), 40 + i,
+                                      0.0, 1.0)
+        for _ in range(2):
+            L.h3_gpu_sdpa_cross_bf16(gpu.h, to, tq, tk, tv, q_rows, kv_rows,
+                                     heads, 128, scale)
+        L.h3_hip_marker(gpu.h, 6)
+        reps = 10
+        for _ in range(reps):
+            if not L.h3_gpu_sdpa_cross_bf16(gpu.h, to, tq, tk, tv, q_rows,
+                                            kv_rows, heads, 128, scale):
+                raise RuntimeError(gpu.error())
+        L.h3_hip_marker(gpu.h, 7)
+        gpu.submit()
+        ms = C.c_double()
+        L.h3_hip_marker_elapsed(gpu.h, 6, 7, C.byref(ms))
+        t = ms.value / reps
+        tf = 4.0 * q_rows * kv_rows * heads * 128 / (t / 1e3) / 1e12
+        out[name] = {"us": round(t * 1e3, 1), "tflops": round(tf, 1),
+                     "frac_of_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+        for t_ in (tq, tk, tv, to):
+            gpu.free(t_)
+    return out
+
+
+def wan_864x480(gpu, blocks, reps):
+    """the Wan-shaped 50-block forward at 864x480x22f
+    (6 x 30 x 54 = 9720 video rows, 512 text rows), weights resident."""
+    rows, text = 6 * 30 * 54, 512
+    cfg = h3hip.dit_config(h3hip.FAMILY_WAN, 5120, 40, 13824, rows,
+                           blocks=blocks, text_rows=text)
+    dit = h3hip.Dit(gpu, cfg)
+    try:
+        dit.init_random(seed=4, weight_std=0.02, mod_std=0.1)
+        cos, sin = rope_tables(wan_positions(6, 30, 54))
+        dit.set_rope(cos, sin)
+        ms, _ = time_forward(gpu, dit, blocks, reps, 1)
+        flops = dit.block_flops()
+        return {"rows": rows, "text_rows": text,
+                "s_per_forward": round(ms / 1e3, 4),
+                "ms_per_block": round(ms / blocks, 3),
+                "tflops": round(blocks * flops / (ms / 1e3) / 1e12, 1),
+                "tflop_per_block": round(flops / 1e12, 3)}
+    finally:
+        dit.close()
+
+
 def load_traffic(name):
     """HBM bytes per launch of the dominant kernel, measured offline with two
     rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) and calibrated on a copy
@@ -310,6 +376,10 @@ def main():
     per_launch_ms = gemm_ms / (blocks * plain_launches)
     dit.close()
 
+    log("attention sweep and the 864x480 forward ...")
+    sweep = attention_sweep(gpu)
+    wan_big = wan_864x480(gpu, blocks, max(2, args.steps // 2))
+
     h3_real = None
     denoise = None
     if not args.no_h3:
@@ -378,6 +448,8 @@ def main():
                      "traffic": load_traffic("gemm_plain_wan512_traffic.json")},
         "h3_real_shape": h3_real,
         "denoise": denoise,
+        "attention_sweep": sweep,
+        "wan_864x480": wan_big,
         "cpu_baseline": base,
     }
     gpu.close()
