@@ -20,16 +20,19 @@
  *   - V is transposed once per tile while being staged into LDS
  *     (V^T rows of 64 keys, 136-byte pitch), K is staged row-major with an
  *     XOR swizzle on 16-byte chunks;
- *   - 4 wave64s x 64 queries = 256 queries per workgroup, 64-key tiles,
+ *   - 8 wave64s x 32 queries = 256 queries per workgroup, 64-key tiles,
  *     double-buffered LDS (2 x 33 KiB) with the next tile's global loads in
- *     flight during the current tile's 64 MFMAs per wave;
+ *     flight during the current tile's 32 MFMAs per wave.  At 32 queries a
+ *     wave needs under 256 registers, so two waves share each SIMD and the
+ *     hardware overlaps one wave's softmax (VALU) with the other's MFMAs;
  *   - the grid is 1-D and regrouped per XCD so the query blocks of one head
  *     run on one XCD and share its L2 copy of that head's K and V;
  *   - the softmax is VALU-bound, so its instruction count is kept low: the
  *     running max only moves (rescaling O and l) when a tile's max exceeds
  *     it by more than 2^8, the scale is folded into one FMA per score, row
- *     maxima use v_max3, and the key-range mask is compiled only into the
- *     last tile's step.
+ *     maxima take two scores per med3 (compiler-visible, so the MFMA ->
+ *     VALU result hazards get their wait states), and the key-range mask
+ *     is compiled only into the last tile's step.
  *
  * A two-pass reference kernel (the reference's naive SDPA,
  * h3_cuda_attention.cu:488-549: one workgroup per (row, head), normalised
@@ -42,7 +45,11 @@
 #include <type_traits>
 
 #define HK_HD 128
-#define HK_QB 256             /* queries per workgroup */
+#define HK_QG 1               /* 32-query groups per wave */
+#define HK_WAVES 8            /* waves per workgroup (two per SIMD) */
+#define HK_THREADS (HK_WAVES * 64)
+#define HK_QB (HK_WAVES * 32 * HK_QG) /* queries per workgroup */
+#define HK_KPT (64 / (HK_THREADS / 16)) /* staged key rows per thread */
 #define HK_KT 64              /* keys per tile */
 #define HK_K_BYTES (HK_KT * HK_HD * 2)        /* 16 KiB, 256-B rows */
 #define HK_VT_PITCH 136                        /* bytes per V^T row */
@@ -74,7 +81,7 @@ struct hk_attn_args {
     int head_major;
 };
 
-__global__ void __launch_bounds__(256, 1) hk_flash_fwd(hk_attn_args a) {
+__global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t hk_lds[];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t col = lane & 31u, half = lane >> 5;
@@ -91,10 +98,10 @@ __global__ void __launch_bounds__(256, 1) hk_flash_fwd(hk_attn_args a) {
 
     /* ---- Q fragments: B operand of S^T = K . Q^T ----
      * group g, k-step ks: Q[q][16 ks + 8 half .. +8] */
-    const uint32_t qbase = qblock * HK_QB + wave * 64u;
-    hk_bf16x8 qf[2][8];
+    const uint32_t qbase = qblock * HK_QB + wave * (32u * HK_QG);
+    hk_bf16x8 qf[HK_QG][8];
 #pragma unroll
-    for (int g = 0; g < 2; g++) {
+    for (int g = 0; g < HK_QG; g++) {
         const uint32_t q = qbase + g * 32u + col;
         const uint32_t off = q < a.q_rows
             ? ((q * row_stride + head * HK_HD + half * 8u) * 2u)
@@ -112,16 +119,16 @@ __global__ void __launch_bounds__(256, 1) hk_flash_fwd(hk_attn_args a) {
      * V: thread t loads chunk dc = t & 15 of key rows 4 kg .. 4 kg + 3,
      *    kg = t >> 4, and writes them transposed */
     const uint32_t sc = tid & 15u, sr = tid >> 4;
-    hk_v4i kreg[4], vreg[4];
+    hk_v4i kreg[HK_KPT], vreg[HK_KPT];
     auto load_tile = [&](uint32_t kv0) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t krow = kv0 + sr + 16u * i;
+        for (int i = 0; i < HK_KPT; i++) {
+            const uint32_t krow = kv0 + sr + (HK_THREADS / 16u) * i;
             const uint32_t koff = krow < a.kv_rows
                 ? ((krow * row_stride + head * HK_HD + sc * 8u) * 2u)
                 : 0xfffffff0u;
             kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 0, 0);
-            const uint32_t vrow = kv0 + sr * 4u + i;
+            const uint32_t vrow = kv0 + sr * HK_KPT + i;
             const uint32_t voff = vrow < a.kv_rows
                 ? ((vrow * row_stride + head * HK_HD + sc * 8u) * 2u)
                 : 0xfffffff0u;
@@ -132,30 +139,41 @@ __global__ void __launch_bounds__(256, 1) hk_flash_fwd(hk_attn_args a) {
         uint8_t *ks = hk_lds + stage * HK_STAGE_BYTES;
         uint8_t *vt = ks + HK_K_BYTES;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            *(hk_v4i *)(ks + hk_k_swz(sr + 16u * i, sc)) = kreg[i];
-        /* transpose 4 keys x 8 dims -> 8 rows of 4 keys */
-        const uint16_t *v16[4];
+        for (int i = 0; i < HK_KPT; i++)
+            *(hk_v4i *)(ks + hk_k_swz(sr + (HK_THREADS / 16u) * i, sc)) =
+                kreg[i];
+        /* transpose KPT keys x 8 dims -> 8 rows of KPT keys */
+        const uint16_t *v16[HK_KPT];
 #pragma unroll
-        for (int i = 0; i < 4; i++) v16[i] = (const uint16_t *)&vreg[i];
+        for (int i = 0; i < HK_KPT; i++) v16[i] = (const uint16_t *)&vreg[i];
 #pragma unroll
         for (int d = 0; d < 8; d++) {
-            uint2 packed;
-            packed.x = (uint32_t)v16[0][d] | ((uint32_t)v16[1][d] << 16);
-            packed.y = (uint32_t)v16[2][d] | ((uint32_t)v16[3][d] << 16);
-            *(uint2 *)(vt + (sc * 8u + d) * HK_VT_PITCH + sr * 8u) = packed;
+            uint8_t *dst = vt + (sc * 8u + d) * HK_VT_PITCH + sr * (2u * HK_KPT);
+            if (HK_KPT == 4) {
+                uint2 packed;
+                packed.x = (uint32_t)v16[0][d] | ((uint32_t)v16[1][d] << 16);
+                packed.y = (uint32_t)v16[2][d] | ((uint32_t)v16[3][d] << 16);
+                *(uint2 *)dst = packed;
+            } else {
+                *(uint32_t *)dst =
+                    (uint32_t)v16[0][d] | ((uint32_t)v16[HK_KPT - 1][d] << 16);
+            }
         }
     };
 
-    hk_f32x16 o[4][2];
+    hk_f32x16 o[4][HK_QG];
 #pragma unroll
     for (int d = 0; d < 4; d++)
 #pragma unroll
-        for (int g = 0; g < 2; g++)
+        for (int g = 0; g < HK_QG; g++)
 #pragma unroll
             for (int r = 0; r < 16; r++) o[d][g][r] = 0.0f;
-    float m_run[2] = {-INFINITY, -INFINITY};
-    float l_part[2] = {0.0f, 0.0f};
+    float m_run[HK_QG], l_part[HK_QG];
+#pragma unroll
+    for (int g = 0; g < HK_QG; g++) {
+        m_run[g] = -INFINITY;
+        l_part[g] = 0.0f;
+    }
 
     const uint32_t tiles = (a.kv_rows + HK_KT - 1) / HK_KT;
     load_tile(0);
@@ -170,11 +188,11 @@ __global__ void __launch_bounds__(256, 1) hk_flash_fwd(hk_attn_args a) {
         const uint8_t *vt = ks + HK_K_BYTES;
 
         /* S^T[kt][g]: keys kt*32 + .., queries g*32 + col */
-        hk_f32x16 s[2][2];
+        hk_f32x16 s[2][HK_QG];
 #pragma unroll
         for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-            for (int g = 0; g < 2; g++)
+            for (int g = 0; g < HK_QG; g++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) s[kt][g][r] = 0.0f;
 #pragma unroll
@@ -184,7 +202,7 @@ __global__ void __launch_bounds__(256, 1) hk_flash_fwd(hk_attn_args a) {
                 hk_bf16x8 kf = *(const hk_bf16x8 *)(
                     ks + hk_k_swz(kt * 32u + col, kk * 2u + half));
 #pragma unroll
-                for (int g = 0; g < 2; g++)
+                for (int g = 0; g < HK_QG; g++)
                     s[kt][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                         kf, qf[g][kk], s[kt][g], 0, 0, 0);
             }
@@ -196,9 +214,9 @@ __global__ void __launch_bounds__(256, 1) hk_flash_fwd(hk_attn_args a) {
          * A power-of-two offset commutes with bf16 rounding, so P and the
          * final O / l match an every-tile rescale up to f32 rounding. */
         const uint32_t kv0 = t * HK_KT;
-        hk_bf16x8 pf[2][2][2]; /* [kt][step][g] */
+        hk_bf16x8 pf[2][2][HK_QG]; /* [kt][step][g] */
 #pragma unroll
-        for (int g = 0; g < 2; g++) {
+        for (int g = 0; g < HK_QG; g++) {
             float mx = -INFINITY;
             if constexpr (tail) {
 #pragma unroll
@@ -214,9 +232,10 @@ __global__ void __launch_bounds__(256, 1) hk_flash_fwd(hk_attn_args a) {
             for (int kt = 0; kt < 2; kt++)
 #pragma unroll
                 for (int r = 0; r < 16; r += 2)
-                    asm("v_max3_f32 %0, %0, %1, %2"
-                        : "+v"(mx)
-                        : "v"(s[kt][g][r]), "v"(s[kt][g][r + 1]));
+                    mx = __builtin_fmaxf(
+                        mx, __builtin_amdgcn_fmed3f(s[kt][g][r],
+                                                    s[kt][g][r + 1],
+                                                    __builtin_inff()));
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * a.scale_log2;
             const bool grow = mx > m_run[g] + 8.0f;
             if (__builtin_amdgcn_ballot_w64(grow)) {
@@ -266,7 +285,7 @@ __global__ void __launch_bounds__(256, 1) hk_flash_fwd(hk_attn_args a) {
                     hk_v4i both = {lo[0], lo[1], hi[0], hi[1]};
                     hk_bf16x8 vf = __builtin_bit_cast(hk_bf16x8, both);
 #pragma unroll
-                    for (int g = 0; g < 2; g++)
+                    for (int g = 0; g < HK_QG; g++)
                         o[d][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                             vf, pf[kt][st][g], o[d][g], 0, 0, 0);
                 }
@@ -282,7 +301,7 @@ __global__ void __launch_bounds__(256, 1) hk_flash_fwd(hk_attn_args a) {
     /* ---- normalise and store: lane owns query column `col` of group g and
      * dims d*32 + (r/4)*8 + 4*half + r%4 */
 #pragma unroll
-    for (int g = 0; g < 2; g++) {
+    for (int g = 0; g < HK_QG; g++) {
         const float l = l_part[g] + __shfl_xor(l_part[g], 32, 64);
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
         const uint32_t q = qbase + g * 32u + col;
@@ -382,7 +401,8 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
         a.kv_bytes = (uint32_t)kv_bytes;
         a.scale_log2 = scale * 1.4426950408889634f;
         a.head_major = head_major;
-        hipLaunchKernelGGL(hk_flash_fwd, dim3(a.q_blocks * heads), dim3(256),
+        hipLaunchKernelGGL(hk_flash_fwd, dim3(a.q_blocks * heads),
+                           dim3(HK_THREADS),
                            HK_ATTN_LDS, gpu->stream, a);
         return 1;
     }
