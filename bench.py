@@ -170,6 +170,18 @@ def h3_measure(gpu, blocks, reps):
         real = {"rows": int(n), "s_per_forward": round(hms / 1e3, 4),
                 "ms_per_block": round(hms / blocks, 3),
                 "tflops": round(blocks * hflops / (hms / 1e3) / 1e12, 1)}
+        # the reference's documented block-sparse window (README H3_SPARSE_ATTN
+        # =16:8:14:8): forward time with the mask, then back to dense
+        kept = L.h3hip_dit_set_sparse_window(hdit.h, C.byref(lay), 16, 8, 14,
+                                             8, 0)
+        if kept < 0:
+            raise RuntimeError(hdit.error())
+        sms, _ = time_forward(gpu, hdit, blocks, reps, 1)
+        L.h3hip_dit_set_sparse_window(hdit.h, None, 0, 0, 0, 0, 1)
+        qb, kt = (n + 127) // 128, (n + 63) // 64
+        real["sparse_16_8_14_8"] = {
+            "tiles_kept_frac": round(kept / (qb * kt), 4),
+            "s_per_forward": round(sms / 1e3, 4)}
         t0 = time.perf_counter()
         evaluations = hdit.denoise()
         seconds = time.perf_counter() - t0

@@ -79,8 +79,13 @@ struct hk_attn_args {
     uint32_t q_bytes, kv_bytes;
     float scale_log2;
     int head_major;
+    /* block-sparse mask: CSR over 128-row query blocks of 64-row key tiles
+     * (lists sorted), or null for dense */
+    const uint32_t *sparse_ptr, *sparse_idx;
+    uint32_t sparse_blocks; /* query blocks in the CSR */
 };
 
+template <bool SPARSE>
 __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t hk_lds[];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
@@ -175,18 +180,62 @@ __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
         l_part[g] = 0.0f;
     }
 
-    const uint32_t tiles = (a.kv_rows + HK_KT - 1) / HK_KT;
-    load_tile(0);
-    store_tile(0);
+    /* ---- key-tile schedule ----
+     * Dense: every 64-key tile in order.  Block-sparse: the workgroup's
+     * 256 queries are two 128-row query blocks of the CSR; it walks the
+     * merged (sorted) union of their tile lists, staging each tile once,
+     * and waves 0-3 (first block) / 4-7 (second block) run the MFMAs and
+     * softmax only on tiles of their own block's list.  A list's length is
+     * clamped to the dense tile count, as in the reference kernel. */
+    const uint32_t dense = (a.kv_rows + HK_KT - 1) / HK_KT;
+    uint32_t dense_next = 0, ia = 0, ea = 0, ib = 0, eb = 0;
+    if (SPARSE) {
+        const uint32_t qa = qblock * 2u, qb = qa + 1u;
+        ia = a.sparse_ptr[qa];
+        ea = min(a.sparse_ptr[qa + 1], ia + dense);
+        if (qb < a.sparse_blocks) {
+            ib = a.sparse_ptr[qb];
+            eb = min(a.sparse_ptr[qb + 1], ib + dense);
+        }
+    }
+    const bool first_block = wave < HK_WAVES / 2;
+    /* next tile of the schedule: false when done; in_a / in_b say whose
+     * list holds it */
+    auto advance = [&](uint32_t &tile, bool &in_a, bool &in_b) -> bool {
+        if (!SPARSE) {
+            if (dense_next >= dense) return false;
+            tile = dense_next++;
+            in_a = in_b = true;
+            return true;
+        }
+        const uint32_t ta = ia < ea ? a.sparse_idx[ia] : 0xffffffffu;
+        const uint32_t tb = ib < eb ? a.sparse_idx[ib] : 0xffffffffu;
+        if (ta == 0xffffffffu && tb == 0xffffffffu) return false;
+        tile = min(ta, tb);
+        in_a = ta == tile;
+        in_b = tb == tile;
+        if (in_a) ia++;
+        if (in_b) ib++;
+        return true;
+    };
+    uint32_t cur = 0, nxt = 0;
+    bool cur_a = false, cur_b = false, nxt_a = false, nxt_b = false;
+    bool have = advance(cur, cur_a, cur_b);
+    if (have) {
+        load_tile(cur * HK_KT);
+        store_tile(0);
+    }
     __syncthreads();
 
-    auto tile_step = [&](uint32_t t, auto tail_tag) {
+    auto tile_step = [&](uint32_t t, uint32_t tile, uint32_t next_tile,
+                         bool more, bool mine, auto tail_tag) {
         constexpr bool tail = decltype(tail_tag)::value;
         const uint32_t stage = t & 1u;
-        if (t + 1 < tiles) load_tile((t + 1) * HK_KT);
+        if (more) load_tile(next_tile * HK_KT);
         const uint8_t *ks = hk_lds + stage * HK_STAGE_BYTES;
         const uint8_t *vt = ks + HK_K_BYTES;
 
+        if (mine) {
         /* S^T[kt][g]: keys kt*32 + .., queries g*32 + col */
         hk_f32x16 s[2][HK_QG];
 #pragma unroll
@@ -213,7 +262,7 @@ __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
          * 2^8 in the exp2 domain; otherwise P = exp2(s - m_stale) <= 256.
          * A power-of-two offset commutes with bf16 rounding, so P and the
          * final O / l match an every-tile rescale up to f32 rounding. */
-        const uint32_t kv0 = t * HK_KT;
+        const uint32_t kv0 = tile * HK_KT;
         hk_bf16x8 pf[2][2][HK_QG]; /* [kt][step][g] */
 #pragma unroll
         for (int g = 0; g < HK_QG; g++) {
@@ -290,13 +339,33 @@ __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
                             vf, pf[kt][st][g], o[d][g], 0, 0, 0);
                 }
             }
+        } /* mine */
 
-        if (t + 1 < tiles) store_tile(stage ^ 1u);
+        if (more) store_tile(stage ^ 1u);
         __syncthreads();
     };
-    for (uint32_t t = 0; t + 1 < tiles; t++)
-        tile_step(t, std::integral_constant<bool, false>());
-    tile_step(tiles - 1, std::integral_constant<bool, true>());
+    /* the key-range mask is compiled only into the step of the last dense
+     * tile, the only tile with keys past kv_rows */
+    if constexpr (!SPARSE) {
+        for (uint32_t t = 0; t + 1 < dense; t++)
+            tile_step(t, t, t + 1, true, true,
+                      std::integral_constant<bool, false>());
+        tile_step(dense - 1, dense - 1, 0, false, true,
+                  std::integral_constant<bool, true>());
+    } else {
+        for (uint32_t t = 0; have; t++) {
+            const bool more = advance(nxt, nxt_a, nxt_b);
+            const bool mine = first_block ? cur_a : cur_b;
+            /* one instantiation (register pressure): the key-range mask is
+             * a no-op except on the last dense tile */
+            tile_step(t, cur, nxt, more, mine,
+                      std::integral_constant<bool, true>());
+            cur = nxt;
+            cur_a = nxt_a;
+            cur_b = nxt_b;
+            have = more;
+        }
+    }
 
     /* ---- normalise and store: lane owns query column `col` of group g and
      * dims d*32 + (r/4)*8 + 4*half + r%4 */
@@ -377,7 +446,8 @@ static bool hk_attn_lds_ready = false;
 int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
                       const uint16_t *k, const uint16_t *v, uint16_t *o,
                       uint32_t q_rows, uint32_t kv_rows, uint32_t heads,
-                      uint32_t head_dim, float scale, int head_major) {
+                      uint32_t head_dim, float scale, int head_major,
+                      int sparse) {
     if (!q_rows || !heads) return 1;
     const uint64_t q_bytes = (uint64_t)q_rows * heads * head_dim * 2;
     const uint64_t kv_bytes = (uint64_t)kv_rows * heads * head_dim * 2;
@@ -388,7 +458,10 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
                        ((uintptr_t)v & 15) == 0 && ((uintptr_t)o & 7) == 0;
     if (flash) {
         if (!hk_attn_lds_ready) {
-            (void)hipFuncSetAttribute((const void *)hk_flash_fwd,
+            (void)hipFuncSetAttribute((const void *)hk_flash_fwd<false>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      HK_ATTN_LDS);
+            (void)hipFuncSetAttribute((const void *)hk_flash_fwd<true>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize,
                                       HK_ATTN_LDS);
             hk_attn_lds_ready = true;
@@ -401,9 +474,19 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
         a.kv_bytes = (uint32_t)kv_bytes;
         a.scale_log2 = scale * 1.4426950408889634f;
         a.head_major = head_major;
-        hipLaunchKernelGGL(hk_flash_fwd, dim3(a.q_blocks * heads),
-                           dim3(HK_THREADS),
-                           HK_ATTN_LDS, gpu->stream, a);
+        const bool masked = sparse && gpu->sparse_ptr &&
+                            gpu->sparse_rows == q_rows && q_rows == kv_rows;
+        a.sparse_ptr = masked ? gpu->sparse_ptr : NULL;
+        a.sparse_idx = masked ? gpu->sparse_idx : NULL;
+        a.sparse_blocks = (q_rows + 127u) / 128u;
+        if (masked)
+            hipLaunchKernelGGL(hk_flash_fwd<true>,
+                               dim3(a.q_blocks * heads), dim3(HK_THREADS),
+                               HK_ATTN_LDS, gpu->stream, a);
+        else
+            hipLaunchKernelGGL(hk_flash_fwd<false>,
+                               dim3(a.q_blocks * heads), dim3(HK_THREADS),
+                               HK_ATTN_LDS, gpu->stream, a);
         return 1;
     }
     if ((size_t)kv_rows * sizeof(float) > 64 * 1024)
@@ -421,7 +504,8 @@ static int hk_sdpa(h3_gpu *gpu, h3_gpu_tensor *output,
                    const h3_gpu_tensor *query, const h3_gpu_tensor *key,
                    const h3_gpu_tensor *value, uint32_t q_rows,
                    uint32_t kv_rows, uint32_t heads, uint32_t head_dim,
-                   float scale, int head_major, const char *name) {
+                   float scale, int head_major, int sparse,
+                   const char *name) {
     size_t q_count = (size_t)q_rows * heads * head_dim;
     size_t kv_count = (size_t)kv_rows * heads * head_dim;
     if (!hk_require(gpu, query, q_count, H3_GPU_BF16, "SDPA query") ||
@@ -433,7 +517,7 @@ static int hk_sdpa(h3_gpu *gpu, h3_gpu_tensor *output,
     hk_op_begin(gpu, name);
     if (!hk_attention_bf16(gpu, HK_CBF16(query), HK_CBF16(key),
                            HK_CBF16(value), HK_BF16(output), q_rows, kv_rows,
-                           heads, head_dim, scale, head_major))
+                           heads, head_dim, scale, head_major, sparse))
         return 0;
     return hk_op_end(gpu, name, HK_KIND_SDPA);
 }
@@ -443,7 +527,7 @@ int h3_gpu_sdpa_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
                      const h3_gpu_tensor *value, uint32_t sequence,
                      uint32_t heads, uint32_t head_dim, float scale) {
     return hk_sdpa(gpu, output, query, key, value, sequence, sequence, heads,
-                   head_dim, scale, 0, "attention");
+                   head_dim, scale, 0, 1, "attention");
 }
 
 int h3_gpu_sdpa_bf16_head_major_output(h3_gpu *gpu, h3_gpu_tensor *output,
@@ -453,7 +537,7 @@ int h3_gpu_sdpa_bf16_head_major_output(h3_gpu *gpu, h3_gpu_tensor *output,
                                        uint32_t sequence, uint32_t heads,
                                        uint32_t head_dim, float scale) {
     return hk_sdpa(gpu, output, query, key, value, sequence, sequence, heads,
-                   head_dim, scale, 1, "attention");
+                   head_dim, scale, 1, 1, "attention");
 }
 
 int h3_gpu_sdpa_cross_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
@@ -463,7 +547,7 @@ int h3_gpu_sdpa_cross_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
                            uint32_t kv_rows, uint32_t heads,
                            uint32_t head_dim, float scale) {
     return hk_sdpa(gpu, output, query, key, value, q_rows, kv_rows, heads,
-                   head_dim, scale, 0, "attention_cross");
+                   head_dim, scale, 0, 0, "attention_cross");
 }
 
 } /* extern "C" */

@@ -55,6 +55,10 @@ struct h3_gpu {
     hipEvent_t markers[16];
     int marker_valid[16];
     int num_cus;
+    /* block-sparse joint attention mask (h3_gpu_sdpa_set_sparse): CSR over
+     * 128-row query blocks of 64-row key tiles, each list sorted */
+    uint32_t *sparse_ptr, *sparse_idx; /* device */
+    uint32_t sparse_rows;
 };
 
 /* stats kinds, mirroring the reference counters (h3_cuda_internal.h:142-160) */
@@ -129,9 +133,12 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *a, const uint16_t *w,
 
 /* Flash attention; q rows [q_rows][heads][hd], k/v [kv_rows][heads][hd].
  * head_major selects [heads][q_rows][hd] output. */
+/* sparse: apply the registered block-sparse mask (joint attention whose
+ * row count matches the registration). */
 int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
                       const uint16_t *k, const uint16_t *v, uint16_t *o,
                       uint32_t q_rows, uint32_t kv_rows, uint32_t heads,
-                      uint32_t head_dim, float scale, int head_major);
+                      uint32_t head_dim, float scale, int head_major,
+                      int sparse);
 
 #endif

@@ -373,6 +373,8 @@ extern "C" void h3_gpu_free(h3_gpu *gpu) {
                 gpu->stats.command_wait_seconds);
     hk_cache_evict(gpu, 0);
     if (gpu->workspace) (void)hipFree(gpu->workspace);
+    if (gpu->sparse_ptr) (void)hipFree(gpu->sparse_ptr);
+    if (gpu->sparse_idx) (void)hipFree(gpu->sparse_idx);
     if (gpu->timing) {
         for (auto &launch : gpu->timing->launches) {
             (void)hipEventDestroy(launch.start);
@@ -396,14 +398,69 @@ extern "C" int h3_gpu_prefers_gpu_sampler(const h3_gpu *gpu) {
     return gpu ? 1 : 0;
 }
 
+/* Block-sparse joint attention (reference h3_gpu.h:44-52,
+ * h3_cuda_attention.cu:1812-1857): validated like the reference (offsets
+ * start at 0, end at idx_count, never decrease; every tile index inside the
+ * dense 64-row tile count), then each query block's list is sorted so the
+ * kernel can walk two neighbouring blocks' lists as one merged sequence. */
+static void hk_sparse_clear(struct h3_gpu *gpu) {
+    if (gpu->sparse_ptr) (void)hipFree(gpu->sparse_ptr);
+    if (gpu->sparse_idx) (void)hipFree(gpu->sparse_idx);
+    gpu->sparse_ptr = NULL;
+    gpu->sparse_idx = NULL;
+    gpu->sparse_rows = 0;
+}
+
+static int hk_u32_compare(const void *a, const void *b) {
+    uint32_t x = *(const uint32_t *)a, y = *(const uint32_t *)b;
+    return x < y ? -1 : x > y;
+}
+
 extern "C" int h3_gpu_sdpa_set_sparse(h3_gpu *gpu, const uint32_t *ptr,
                                       size_t ptr_count, const uint32_t *idx,
                                       size_t idx_count, uint32_t rows) {
-    (void)ptr; (void)ptr_count; (void)idx; (void)idx_count; (void)rows;
-    /* The caller keeps dense attention when registration fails
-     * (reference h3_dit.c:1122-1129). */
-    return hk_fail(gpu, "block-sparse attention is not available on the "
-                        "HIP backend");
+    if (!gpu) return 0;
+    if (gpu->active && hipStreamSynchronize(gpu->stream) != hipSuccess)
+        return hk_fail(gpu, "cannot synchronise before replacing the mask");
+    hk_sparse_clear(gpu);
+    if (!ptr) return 1; /* cleared */
+    if (!idx || !ptr_count || !idx_count || !rows)
+        return hk_fail(gpu, "invalid block-sparse attention mask");
+    const uint32_t ktiles = (rows + 63u) / 64u;
+    if (ptr[0] != 0 || ptr[ptr_count - 1] != (uint32_t)idx_count)
+        return hk_fail(gpu, "block-sparse mask offsets are inconsistent");
+    for (size_t i = 1; i < ptr_count; i++)
+        if (ptr[i] < ptr[i - 1])
+            return hk_fail(gpu, "block-sparse mask offsets decrease");
+    for (size_t i = 0; i < idx_count; i++)
+        if (idx[i] >= ktiles)
+            return hk_fail(gpu, "block-sparse mask tile %u outside %u tiles",
+                           idx[i], ktiles);
+    if (ptr_count - 1 < (rows + 127u) / 128u)
+        return hk_fail(gpu, "block-sparse mask has %zu query blocks, %u "
+                            "rows need %u", ptr_count - 1, rows,
+                       (rows + 127u) / 128u);
+    uint32_t *sorted = (uint32_t *)malloc(idx_count * sizeof(uint32_t));
+    if (!sorted) return hk_fail(gpu, "out of memory");
+    memcpy(sorted, idx, idx_count * sizeof(uint32_t));
+    for (size_t q = 0; q + 1 < ptr_count; q++)
+        qsort(sorted + ptr[q], ptr[q + 1] - ptr[q], sizeof(uint32_t),
+              hk_u32_compare);
+    int ok = hipMalloc((void **)&gpu->sparse_ptr,
+                       ptr_count * sizeof(uint32_t)) == hipSuccess &&
+             hipMalloc((void **)&gpu->sparse_idx,
+                       idx_count * sizeof(uint32_t)) == hipSuccess &&
+             hipMemcpy(gpu->sparse_ptr, ptr, ptr_count * sizeof(uint32_t),
+                       hipMemcpyHostToDevice) == hipSuccess &&
+             hipMemcpy(gpu->sparse_idx, sorted, idx_count * sizeof(uint32_t),
+                       hipMemcpyHostToDevice) == hipSuccess;
+    free(sorted);
+    if (!ok) {
+        hk_sparse_clear(gpu);
+        return hk_fail(gpu, "cannot upload the block-sparse mask");
+    }
+    gpu->sparse_rows = rows;
+    return 1;
 }
 
 /* -------------------------------------------------------------- tensors */

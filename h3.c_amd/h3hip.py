@@ -190,6 +190,13 @@ def lib():
         "h3hip_dit_forward_step": (_I, [_P, _I]),
         "h3hip_dit_denoise": (_I, [_P]),
         "h3hip_dit_schedule_precompute": (_I, [_P, C.c_uint64, _F]),
+        "h3hip_dit_set_sparse_window": (C.c_long, [_P, C.POINTER(Layout),
+                                                   C.c_uint, C.c_uint,
+                                                   C.c_uint, C.c_uint, _I]),
+        "h3hip_sparse_mask": (C.c_long, [C.POINTER(Layout), C.c_uint,
+                                         C.c_uint, C.c_uint, C.c_uint, _P,
+                                         _P, _SZ]),
+        "h3_gpu_sdpa_set_sparse": (_I, [_P, _P, _SZ, _P, _SZ, _U32]),
         "h3hip_dit_sampler_rows": (None, [_P, C.POINTER(_U32),
                                           C.POINTER(_U32), C.POINTER(_U32),
                                           C.POINTER(_U32)]),

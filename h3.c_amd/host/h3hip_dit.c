@@ -1125,3 +1125,46 @@ int h3hip_dit_schedule_precompute(h3hip_dit *dit, uint64_t seed,
         h3_gpu_tensor_free(temps[i]);
     return ok;
 }
+
+/* ------------------------------------------------- sparse attention */
+
+long h3hip_dit_set_sparse_window(h3hip_dit *dit, const h3hip_layout *layout,
+                                 unsigned radius_t, unsigned radius_h,
+                                 unsigned radius_w, unsigned global_stride,
+                                 int clear) {
+    if (!dit) return -1;
+    if (clear)
+        return h3_gpu_sdpa_set_sparse(dit->gpu, NULL, 0, NULL, 0, 0)
+                   ? 0 : (dit_fail(dit, "clear mask: %s",
+                                   h3_gpu_error(dit->gpu)), -1);
+    if (!layout || layout->seq_len != dit->config.rows) {
+        dit_fail(dit, "the mask's layout must match the DiT rows");
+        return -1;
+    }
+    const size_t qblocks = (layout->seq_len + 127) / 128;
+    uint32_t *ptr = (uint32_t *)malloc((qblocks + 1) * sizeof(uint32_t));
+    if (!ptr) return (dit_fail(dit, "out of memory"), -1);
+    long total = h3hip_sparse_mask(layout, radius_t, radius_h, radius_w,
+                                   global_stride, ptr, NULL, 0);
+    if (total < 0) {
+        free(ptr);
+        return 0; /* no single target video segment: stays dense */
+    }
+    uint32_t *idx = (uint32_t *)malloc((total ? total : 1) * sizeof(uint32_t));
+    if (!idx) {
+        free(ptr);
+        return (dit_fail(dit, "out of memory"), -1);
+    }
+    (void)h3hip_sparse_mask(layout, radius_t, radius_h, radius_w,
+                            global_stride, ptr, idx, (size_t)total);
+    int ok = total > 0 &&
+             h3_gpu_sdpa_set_sparse(dit->gpu, ptr, qblocks + 1, idx,
+                                    (size_t)total, dit->config.rows);
+    free(ptr);
+    free(idx);
+    if (!ok) {
+        dit_fail(dit, "sparse mask: %s", h3_gpu_error(dit->gpu));
+        return -1;
+    }
+    return total;
+}

@@ -176,6 +176,18 @@ int h3hip_dit_denoise(h3hip_dit *dit);
 int h3hip_dit_schedule_precompute(h3hip_dit *dit, uint64_t seed,
                                   float weight_std);
 
+/* Opt-in block-sparse joint attention, the reference's H3_SPARSE_ATTN=T:H:W:G
+ * (h3_dit.c:1006-1132): builds the layout's CSR window mask
+ * (h3hip_sparse_mask) and registers it with h3_gpu_sdpa_set_sparse, so
+ * every joint attention over config.rows rows is masked.  Radii 0 with
+ * global_stride 0 and clear = 1 removes the mask.  Outside a batch.
+ * Returns the kept-tile count, 0 when the layout has no single target
+ * video segment (attention stays dense), -1 on failure. */
+long h3hip_dit_set_sparse_window(h3hip_dit *dit, const h3hip_layout *layout,
+                                 unsigned radius_t, unsigned radius_h,
+                                 unsigned radius_w, unsigned global_stride,
+                                 int clear);
+
 /* Rows of each latent array: video / audio totals and their targets. */
 void h3hip_dit_sampler_rows(const h3hip_dit *dit, uint32_t *video_rows,
                             uint32_t *audio_rows, uint32_t *video_targets,

@@ -3,6 +3,7 @@
  * positions, RoPE tables and row maps must match bit for bit. */
 #include "h3hip_host.h"
 
+#include <limits.h>
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -662,4 +663,81 @@ float h3hip_bf16_to_f32(uint16_t value) {
     float out;
     memcpy(&out, &bits, 4);
     return out;
+}
+
+/* ------------------------------------------------ block-sparse attention */
+
+typedef struct {
+    int global, min_t, max_t, min_h, max_h, min_w, max_w;
+} hh_box;
+
+static int hh_gap(int qmin, int qmax, int kmin, int kmax) {
+    return kmin > qmax ? kmin - qmax : qmin > kmax ? qmin - kmax : 0;
+}
+
+long h3hip_sparse_mask(const h3hip_layout *layout, unsigned radius_t,
+                       unsigned radius_h, unsigned radius_w,
+                       unsigned global_stride, uint32_t *ptr, uint32_t *idx,
+                       size_t idx_capacity) {
+    if (!layout || !ptr || !layout->positions) return -1;
+    size_t video_start = 0, video_stop = 0;
+    unsigned video_segments = 0;
+    for (size_t i = 0; i < layout->segment_count; i++)
+        if (layout->segments[i].kind == H3HIP_SEG_VIDEO) {
+            video_start = layout->segments[i].start;
+            video_stop = layout->segments[i].stop;
+            video_segments++;
+        }
+    if (video_segments != 1) return -1;
+    const size_t rows = layout->seq_len;
+    const size_t qblocks = (rows + 127) / 128, ktiles = (rows + 63) / 64;
+    hh_box *boxes = (hh_box *)calloc(qblocks + ktiles, sizeof(hh_box));
+    if (!boxes) return -1;
+    hh_box *qbox = boxes, *kbox = boxes + qblocks;
+    for (size_t b = 0; b < qblocks + ktiles; b++) {
+        boxes[b].min_t = boxes[b].min_h = boxes[b].min_w = INT_MAX;
+        boxes[b].max_t = boxes[b].max_h = boxes[b].max_w = INT_MIN;
+    }
+    for (size_t row = 0; row < rows; row++) {
+        hh_box *sides[2] = {&qbox[row / 128], &kbox[row / 64]};
+        for (int side = 0; side < 2; side++) {
+            hh_box *box = sides[side];
+            if (row < video_start || row >= video_stop) {
+                box->global = 1;
+                continue;
+            }
+            const int t = (int)lrint(layout->positions[row].t);
+            const int h = (int)lrint(layout->positions[row].h);
+            const int w = (int)lrint(layout->positions[row].w);
+            if (t < box->min_t) box->min_t = t;
+            if (t > box->max_t) box->max_t = t;
+            if (h < box->min_h) box->min_h = h;
+            if (h > box->max_h) box->max_h = h;
+            if (w < box->min_w) box->min_w = w;
+            if (w > box->max_w) box->max_w = w;
+        }
+    }
+    size_t at = 0;
+    for (size_t q = 0; q < qblocks; q++) {
+        ptr[q] = (uint32_t)at;
+        for (size_t k = 0; k < ktiles; k++) {
+            int keep = qbox[q].global || kbox[k].global ||
+                       (global_stride && k % global_stride == 0);
+            if (!keep && qbox[q].min_t <= qbox[q].max_t &&
+                kbox[k].min_t <= kbox[k].max_t)
+                keep = hh_gap(qbox[q].min_t, qbox[q].max_t, kbox[k].min_t,
+                              kbox[k].max_t) <= (int)radius_t &&
+                       hh_gap(qbox[q].min_h, qbox[q].max_h, kbox[k].min_h,
+                              kbox[k].max_h) <= (int)radius_h &&
+                       hh_gap(qbox[q].min_w, qbox[q].max_w, kbox[k].min_w,
+                              kbox[k].max_w) <= (int)radius_w;
+            if (keep) {
+                if (idx && at < idx_capacity) idx[at] = (uint32_t)k;
+                at++;
+            }
+        }
+    }
+    ptr[qblocks] = (uint32_t)at;
+    free(boxes);
+    return (long)at;
 }

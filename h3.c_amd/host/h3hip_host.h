@@ -117,6 +117,20 @@ int h3hip_row_map(const h3hip_layout *layout, uint32_t video_row,
                   uint32_t audio_condition_row, const uint8_t *text_tags,
                   size_t text_tag_count, uint32_t *rows, size_t row_count);
 
+/* Block-sparse attention mask of a packed layout (reference
+ * h3_dit.c:1006-1132): a CSR over 128-row query blocks of 64-row key
+ * tiles.  Target-video tiles attend within a 3D window of the given radii
+ * (latent-patch units, positions rounded with lrint) plus every
+ * global_stride-th tile (0 disables); a tile holding any text, audio,
+ * condition or reference row is global in both directions.  ptr receives
+ * qblocks + 1 offsets; idx (when idx_capacity suffices) the tile lists.
+ * Returns the number of kept tiles, or -1 when the layout has no single
+ * target video segment (the reference then stays dense). */
+long h3hip_sparse_mask(const h3hip_layout *layout, unsigned radius_t,
+                       unsigned radius_h, unsigned radius_w,
+                       unsigned global_stride, uint32_t *ptr, uint32_t *idx,
+                       size_t idx_capacity);
+
 /* Evaluated steps under velocity reuse (reference h3_dit.c:2672-2687). */
 int h3hip_reuse_schedule(int steps, int reuse_interval, uint8_t *selected,
                          size_t selected_count);

@@ -398,6 +398,67 @@ void orc_sdpa(const bf16 *q, const bf16 *k, const bf16 *v, bf16 *out,
     }
 }
 
+/* Block-sparse joint attention (reference h3_gpu.h:44-52, the FA2 kernel's
+ * CSR walk h3_cuda_attention.cu:1652-1673): query row r of block r / 128
+ * attends only to the keys of the 64-row tiles listed for its block, with
+ * the same softmax as orc_sdpa (max over the kept keys, P rounded to bf16
+ * before P.V when round_p).  Lists are clamped to the dense tile count. */
+void orc_sdpa_sparse(const bf16 *q, const bf16 *k, const bf16 *v, bf16 *out,
+                     size_t rows, size_t heads, size_t hd, float scale,
+                     int head_major, int round_p, const uint32_t *ptr,
+                     const uint32_t *idx) {
+    const size_t tiles = (rows + 63) / 64;
+#pragma omp parallel
+    {
+        float *s = (float *)malloc((rows ? rows : 1) * sizeof(float));
+        unsigned char *keep = (unsigned char *)malloc(tiles ? tiles : 1);
+        float *qf = (float *)malloc(hd * sizeof(float));
+        float *acc = (float *)malloc(hd * sizeof(float));
+#pragma omp for schedule(dynamic, 4)
+        for (size_t i = 0; i < rows * heads; i++) {
+            const size_t row = i / heads, head = i % heads;
+            const size_t block = row / 128;
+            memset(keep, 0, tiles ? tiles : 1);
+            size_t count = ptr[block + 1] - ptr[block];
+            if (count > tiles) count = tiles;
+            for (size_t t = 0; t < count; t++) keep[idx[ptr[block] + t]] = 1;
+            const size_t qb = (row * heads + head) * hd;
+            for (size_t d = 0; d < hd; d++) qf[d] = b2f(q[qb + d]);
+            float mx = -INFINITY;
+            for (size_t j = 0; j < rows; j++) {
+                if (!keep[j / 64]) continue;
+                const bf16 *kr = k + (j * heads + head) * hd;
+                float dot = 0.0f;
+                for (size_t d = 0; d < hd; d++) dot = fmaf(qf[d], b2f(kr[d]), dot);
+                s[j] = dot * scale;
+                if (s[j] > mx) mx = s[j];
+            }
+            float l = 0.0f;
+            for (size_t j = 0; j < rows; j++) {
+                if (!keep[j / 64]) continue;
+                s[j] = expf(s[j] - mx);
+                l += s[j];
+            }
+            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+            for (size_t d = 0; d < hd; d++) acc[d] = 0.0f;
+            for (size_t j = 0; j < rows; j++) {
+                if (!keep[j / 64]) continue;
+                const bf16 *vr = v + (j * heads + head) * hd;
+                const float p = round_p ? rbf(s[j]) : s[j] * inv;
+                for (size_t d = 0; d < hd; d++)
+                    acc[d] = fmaf(p, b2f(vr[d]), acc[d]);
+            }
+            const size_t ob = head_major ? (head * rows + row) * hd : qb;
+            for (size_t d = 0; d < hd; d++)
+                out[ob + d] = f2b(round_p ? acc[d] * inv : acc[d]);
+        }
+        free(s);
+        free(keep);
+        free(qf);
+        free(acc);
+    }
+}
+
 /* ------------------------------------------------------- elementwise */
 
 static inline float silu(float x) { return x / (1.0f + expf(-x)); }

@@ -36,6 +36,8 @@ def lib():
         sig = {
             "orc_linear_bf16": [_P, _P, _P, _P, _SZ, _SZ, _SZ],
             "orc_linear_f32": [_P, _P, _P, _P, _SZ, _SZ, _SZ],
+            "orc_sdpa_sparse": [_P, _P, _P, _P, _SZ, _SZ, _SZ, _F, C.c_int,
+                                C.c_int, _P, _P],
             "orc_patch_linear": [_P, _P, _P, _P, _P, _SZ, _SZ, _SZ],
             "orc_adaln": [_P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _F],
             "orc_gate": [_P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _SZ],
@@ -209,6 +211,19 @@ def sdpa(q, k, v, q_rows, kv_rows, heads, hd, scale, head_major=False,
     return out
 
 
+def sdpa_sparse(q, k, v, rows, heads, hd, scale, ptr, idx,
+                head_major=False, round_p=True):
+    """Block-sparse joint attention over a CSR of 64-row key tiles per
+    128-row query block (h3_gpu.h:44-52; h3_cuda_attention.cu:1652-1673)."""
+    out = np.empty(rows * heads * hd, np.uint16)
+    p = np.ascontiguousarray(ptr, dtype=np.uint32)
+    i = np.ascontiguousarray(idx, dtype=np.uint32)
+    lib().orc_sdpa_sparse(_p(_u16(q)), _p(_u16(k)), _p(_u16(v)), _p(out),
+                          rows, heads, hd, scale, int(head_major),
+                          int(round_p), _p(p), _p(i))
+    return out
+
+
 def swiglu(fused, rows, width):
     """h3_cuda_core.cu:104-114."""
     out = np.empty(rows * width, np.uint16)
@@ -277,11 +292,12 @@ def ffn_gelu(x, fc1, b1, fc2, b2, rows, d, ffn):
 # ---------------------------------------------------------- block orders
 
 def h3_blocks(hidden, blocks, row_map, cos, sin, rows, hidden_dim, heads, ffn,
-              hd=128, rope_half=48, eps=1e-5):
+              hd=128, rope_half=48, eps=1e-5, sparse=None):
     """Consecutive H3 blocks in the reference run order (h3_dit.c:2008-2180,
     BF16 path; fused gate+adaLN; the MLP gate of block i fused with block
     i+1's attention adaLN, :2139-2178).  blocks: list of dicts with norm1,
     norm2, qkv, q_norm, k_norm, out, fc1, fc2, modulation (bf16 bits).
+    sparse: optional (ptr, idx) block-sparse mask of the joint attention.
     Returns the final hidden state."""
     S = 6
     inner = heads * hd
@@ -295,7 +311,11 @@ def h3_blocks(hidden, blocks, row_map, cos, sin, rows, hidden_dim, heads, ffn,
         qkv = linear(a, w["qkv"], None, rows, hidden_dim, 3 * inner)
         q, k, v = qkv_rope(qkv, w["q_norm"], w["k_norm"], cos, sin, rows,
                            heads, hd, rope_half, True, eps)
-        o = sdpa(q, k, v, rows, rows, heads, hd, 1.0 / math.sqrt(hd))
+        if sparse is None:
+            o = sdpa(q, k, v, rows, rows, heads, hd, 1.0 / math.sqrt(hd))
+        else:
+            o = sdpa_sparse(q, k, v, rows, heads, hd, 1.0 / math.sqrt(hd),
+                            sparse[0], sparse[1])
         y = linear(o, w["out"], None, rows, inner, hidden_dim)
         x, b = gate_adaln(x, y, w["norm2"], mod, mod, row_map, rows,
                           hidden_dim, S, 2, 3, 4, eps)
