@@ -680,6 +680,171 @@ __global__ void hk_fill_normal_kernel(T *out, size_t count, uint64_t seed,
 
 /* =============================================================== host */
 
+/* ---------------------------------------------------------------------
+ * Token reduction (reference h3_cuda_dit.cu:336-535): pool pairs of rows of
+ * the full token grid into one reduced row, snapshot the pre-pool rows
+ * ("original") and the pooled rows the reduced stack starts from
+ * ("baseline"); later expand back, each full row taking its parent's update
+ * relative to that baseline.  The _adaln variants fuse the next attention
+ * RMS adaLN.  One workgroup per output row; rows are moved in 16-byte
+ * chunks when the width allows.  Every row addressed through a device-side
+ * index (pairs, parents, baseline rows) goes through a buffer resource
+ * bounded by its tensor, so a bad index reads zeros and drops its writes
+ * instead of faulting.
+ * ------------------------------------------------------------------- */
+struct hk_token_args {
+    const uint16_t *input;     /* pool: full grid; expand: reduced stack */
+    uint16_t *original;        /* full-grid snapshot */
+    uint16_t *baseline;        /* pooled snapshot rows */
+    const uint32_t *baseline_indices;
+    const uint32_t *index;     /* pool: pairs (2 per row); expand: parents */
+    uint16_t *residual;        /* pool: reduced rows; expand: full rows */
+    uint16_t *adaln;           /* fused adaLN output or null */
+    const uint16_t *norm_weight, *modulation;
+    const uint32_t *row_map;
+    uint32_t input_bytes, original_bytes, baseline_bytes, index_bytes,
+        baseline_index_bytes;
+    uint32_t input_offset, original_offset, baseline_offset; /* elements */
+    uint32_t rows, width, exact_prefix_rows;
+    uint32_t slots, shift_slot, scale_slot;
+    float update_scale, epsilon;
+};
+
+typedef int hk_v4i __attribute__((ext_vector_type(4)));
+
+#define HK_TOKEN_CHUNKS 3 /* 16-byte chunks per thread: width <= 6144 */
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t hk_tok_rsrc(const void *p,
+                                                              uint32_t n) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0,
+                                             (int)n, 0x00020000);
+}
+
+/* EXPAND = false: pool; true: expand.  ADALN: fuse the RMS adaLN. */
+template <bool EXPAND, bool ADALN>
+__global__ void __launch_bounds__(256)
+hk_token_kernel(hk_token_args a) {
+    __shared__ float scratch[16];
+    const uint32_t row = blockIdx.x;
+    const uint32_t width = a.width, chunks = width >> 3;
+    const auto in_r = hk_tok_rsrc(a.input, a.input_bytes);
+    const auto org_r = hk_tok_rsrc(a.original, a.original_bytes);
+    const auto base_r = hk_tok_rsrc(a.baseline, a.baseline_bytes);
+    const auto idx_r = hk_tok_rsrc(a.index, a.index_bytes);
+    const auto bidx_r = hk_tok_rsrc(a.baseline_indices, a.baseline_index_bytes);
+    uint32_t first, second, baseline_row;
+    bool direct = false;
+    if (!EXPAND) {
+        first = __builtin_amdgcn_raw_buffer_load_b32(idx_r, row * 8u, 0, 0);
+        second = __builtin_amdgcn_raw_buffer_load_b32(idx_r, row * 8u + 4u,
+                                                      0, 0);
+        baseline_row = __builtin_amdgcn_raw_buffer_load_b32(bidx_r, row * 4u,
+                                                            0, 0);
+    } else {
+        first = __builtin_amdgcn_raw_buffer_load_b32(idx_r, row * 4u, 0, 0);
+        second = first;
+        baseline_row = __builtin_amdgcn_raw_buffer_load_b32(bidx_r, first * 4u,
+                                                            0, 0);
+        direct = row < a.exact_prefix_rows || baseline_row == 0xffffffffu;
+    }
+    /* byte offsets of the rows this workgroup touches */
+    const uint32_t in1 = (a.input_offset + first * width) * 2u;
+    const uint32_t in2 = (a.input_offset + second * width) * 2u;
+    const uint32_t org1 = (a.original_offset +
+                           (EXPAND ? row : first) * width) * 2u;
+    const uint32_t org2 = (a.original_offset + second * width) * 2u;
+    const uint32_t bas = baseline_row == 0xffffffffu
+        ? 0xfffffff0u
+        : (a.baseline_offset + baseline_row * width) * 2u;
+    uint16_t *dst = a.residual + (size_t)row * width;
+
+    float local = 0.0f;
+    hk_v4i kept[HK_TOKEN_CHUNKS];
+#pragma unroll
+    for (int j = 0; j < HK_TOKEN_CHUNKS; j++) {
+        const uint32_t c = threadIdx.x + j * 256u;
+        if (c >= chunks) break;
+        const uint32_t cb = c * 16u;
+        hk_v4i value;
+        if (!EXPAND) {
+            hk_v4i x = __builtin_amdgcn_raw_buffer_load_b128(in_r, in1 + cb,
+                                                              0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(x, org_r, org1 + cb, 0, 0);
+            value = x;
+            if (first != second) {
+                hk_v4i y = __builtin_amdgcn_raw_buffer_load_b128(
+                    in_r, in2 + cb, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(y, org_r, org2 + cb, 0,
+                                                       0);
+                const uint16_t *xs = (const uint16_t *)&x;
+                const uint16_t *ys = (const uint16_t *)&y;
+                uint16_t *vs = (uint16_t *)&value;
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    vs[e] = hk_f2bf((hk_bf2f(xs[e]) + hk_bf2f(ys[e])) * 0.5f);
+            }
+            if (baseline_row != 0xffffffffu)
+                __builtin_amdgcn_raw_buffer_store_b128(value, base_r,
+                                                       bas + cb, 0, 0);
+        } else {
+            value = __builtin_amdgcn_raw_buffer_load_b128(in_r, in1 + cb, 0,
+                                                          0);
+            if (!direct) {
+                hk_v4i o = __builtin_amdgcn_raw_buffer_load_b128(
+                    org_r, org1 + cb, 0, 0);
+                hk_v4i b = __builtin_amdgcn_raw_buffer_load_b128(
+                    base_r, bas + cb, 0, 0);
+                const uint16_t *os = (const uint16_t *)&o;
+                const uint16_t *bs = (const uint16_t *)&b;
+                uint16_t *vs = (uint16_t *)&value;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float update = hk_bf2f(vs[e]) - hk_bf2f(bs[e]);
+                    vs[e] = hk_f2bf(hk_bf2f(os[e]) + a.update_scale * update);
+                }
+            }
+        }
+        *(hk_v4i *)(dst + c * 8u) = value;
+        if (ADALN) {
+            kept[j] = value;
+            const uint16_t *vs = (const uint16_t *)&value;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float f = hk_bf2f(vs[e]);
+                local = fmaf(f, f, local);
+            }
+        }
+    }
+    if (!ADALN) return;
+    const float total = hk_block_sum(local, scratch);
+    const float inverse = 1.0f / sqrtf(total / (float)width + a.epsilon);
+    const size_t base = (size_t)a.row_map[row] * a.slots * width;
+    const uint16_t *shift = a.modulation + base + (size_t)a.shift_slot * width;
+    const uint16_t *scale = a.modulation + base + (size_t)a.scale_slot * width;
+    uint16_t *out = a.adaln + (size_t)row * width;
+#pragma unroll
+    for (int j = 0; j < HK_TOKEN_CHUNKS; j++) {
+        const uint32_t c = threadIdx.x + j * 256u;
+        if (c >= chunks) break;
+        const uint16_t *vs = (const uint16_t *)&kept[j];
+        const hk_v4i w = *(const hk_v4i *)(a.norm_weight + c * 8u);
+        const hk_v4i sh = *(const hk_v4i *)(shift + c * 8u);
+        const hk_v4i sc = *(const hk_v4i *)(scale + c * 8u);
+        const uint16_t *ws = (const uint16_t *)&w;
+        const uint16_t *shs = (const uint16_t *)&sh;
+        const uint16_t *scs = (const uint16_t *)&sc;
+        hk_v4i result;
+        uint16_t *rs = (uint16_t *)&result;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float normalized = hk_bf2f(vs[e]) * inverse * hk_bf2f(ws[e]);
+            rs[e] = hk_f2bf(normalized * (1.0f + hk_bf2f(scs[e])) +
+                            hk_bf2f(shs[e]));
+        }
+        *(hk_v4i *)(out + c * 8u) = result;
+    }
+}
+
 #define HK_REQ_BF16(t, n, label) hk_require(gpu, t, n, H3_GPU_BF16, label)
 #define HK_REQ_F32(t, n, label) hk_require(gpu, t, n, H3_GPU_F32, label)
 #define HK_REQ_U32(t, n, label) hk_require(gpu, t, n, H3_GPU_U32, label)
@@ -1510,3 +1675,255 @@ int h3_gpu_fill_normal_f32(h3_gpu *gpu, h3_gpu_tensor *tensor, size_t offset,
 }
 
 } /* extern "C" */
+
+/* ------------------------------------------------------ token reduction */
+
+static int hk_token_fits(const h3_gpu_tensor *t, size_t offset, size_t count,
+                         h3_gpu_dtype dtype) {
+    return t && t->dtype == dtype && offset <= t->elements &&
+           count <= t->elements - offset && t->bytes < 0xfffff000ull;
+}
+
+static int hk_token_launch(h3_gpu *gpu, bool expand, bool adaln,
+                           hk_token_args &a, const char *name) {
+    hk_op_begin(gpu, name);
+    if (a.rows) {
+        if (!expand && !adaln)
+            hipLaunchKernelGGL((hk_token_kernel<false, false>), dim3(a.rows),
+                               dim3(256), 0, gpu->stream, a);
+        else if (!expand)
+            hipLaunchKernelGGL((hk_token_kernel<false, true>), dim3(a.rows),
+                               dim3(256), 0, gpu->stream, a);
+        else if (!adaln)
+            hipLaunchKernelGGL((hk_token_kernel<true, false>), dim3(a.rows),
+                               dim3(256), 0, gpu->stream, a);
+        else
+            hipLaunchKernelGGL((hk_token_kernel<true, true>), dim3(a.rows),
+                               dim3(256), 0, gpu->stream, a);
+    }
+    return hk_op_end(gpu, name, HK_KIND_DIRECT);
+}
+
+/* Shared validation of the pool ops (reference h3_cuda_dit.cu:797-921). */
+static int hk_pool_setup(h3_gpu *gpu, hk_token_args &a, h3_gpu_tensor *output,
+                         const h3_gpu_tensor *input, size_t input_offset,
+                         h3_gpu_tensor *original, size_t original_offset,
+                         h3_gpu_tensor *baseline, size_t baseline_offset,
+                         const h3_gpu_tensor *baseline_indices,
+                         const h3_gpu_tensor *pairs, uint32_t input_rows,
+                         uint32_t rows, uint32_t baseline_rows,
+                         uint32_t width, const char *what) {
+    const size_t elements = (size_t)rows * width;
+    const size_t input_elements = (size_t)input_rows * width;
+    const size_t baseline_elements = (size_t)baseline_rows * width;
+    if (!input_rows || !rows || rows > input_rows || baseline_rows > rows ||
+        !width || elements > UINT32_MAX || input_offset > UINT32_MAX ||
+        input_elements > UINT32_MAX - input_offset ||
+        original_offset > UINT32_MAX ||
+        input_elements > UINT32_MAX - original_offset ||
+        baseline_offset > UINT32_MAX ||
+        baseline_elements > UINT32_MAX - baseline_offset)
+        return hk_fail(gpu, "%s shape is out of range", what);
+    if (width % 8 || width > 256 * 8 * HK_TOKEN_CHUNKS)
+        return hk_fail(gpu, "%s width must be a multiple of 8 up to %d", what,
+                       256 * 8 * HK_TOKEN_CHUNKS);
+    if (!hk_token_fits(input, input_offset, input_elements, H3_GPU_BF16))
+        return hk_fail(gpu, "%s input tensor is too small", what);
+    if (!hk_token_fits(original, original_offset, input_elements,
+                       H3_GPU_BF16))
+        return hk_fail(gpu, "%s original tensor is too small", what);
+    if (!hk_token_fits(baseline, baseline_offset, baseline_elements,
+                       H3_GPU_BF16))
+        return hk_fail(gpu, "%s baseline tensor is too small", what);
+    if (!HK_REQ_BF16(output, elements, "token pool output") ||
+        !HK_REQ_U32(baseline_indices, rows, "token pool baseline indices") ||
+        !HK_REQ_U32(pairs, (size_t)rows * 2, "token pool pairs") ||
+        !hk_require_active(gpu))
+        return 0;
+    memset(&a, 0, sizeof(a));
+    a.input = HK_CBF16(input);
+    a.original = HK_BF16(original);
+    a.baseline = HK_BF16(baseline);
+    a.baseline_indices = HK_CU32(baseline_indices);
+    a.index = HK_CU32(pairs);
+    a.residual = HK_BF16(output);
+    a.input_bytes = (uint32_t)input->bytes;
+    a.original_bytes = (uint32_t)original->bytes;
+    a.baseline_bytes = (uint32_t)baseline->bytes;
+    a.index_bytes = (uint32_t)pairs->bytes;
+    a.baseline_index_bytes = (uint32_t)baseline_indices->bytes;
+    a.input_offset = (uint32_t)input_offset;
+    a.original_offset = (uint32_t)original_offset;
+    a.baseline_offset = (uint32_t)baseline_offset;
+    a.rows = rows;
+    a.width = width;
+    return 1;
+}
+
+static int hk_adaln_setup(h3_gpu *gpu, hk_token_args &a, h3_gpu_tensor *out,
+                          const h3_gpu_tensor *norm_weight,
+                          const h3_gpu_tensor *modulation,
+                          const h3_gpu_tensor *row_map, uint32_t rows,
+                          uint32_t width, uint32_t slots, uint32_t shift_slot,
+                          uint32_t scale_slot, float epsilon,
+                          const char *what) {
+    if (width > 5376)
+        return hk_fail(gpu, "%s width is out of range", what);
+    if (shift_slot >= slots || scale_slot >= slots)
+        return hk_fail(gpu, "%s modulation slot out of range", what);
+    if (!HK_REQ_BF16(norm_weight, width, "fused token adaLN norm") ||
+        !HK_REQ_BF16(modulation, 1, "fused token adaLN modulation") ||
+        !HK_REQ_U32(row_map, rows, "fused token adaLN row map") ||
+        !HK_REQ_BF16(out, (size_t)rows * width, "fused token adaLN output"))
+        return 0;
+    a.adaln = HK_BF16(out);
+    a.norm_weight = HK_CBF16(norm_weight);
+    a.modulation = HK_CBF16(modulation);
+    a.row_map = HK_CU32(row_map);
+    a.slots = slots;
+    a.shift_slot = shift_slot;
+    a.scale_slot = scale_slot;
+    a.epsilon = epsilon;
+    return 1;
+}
+
+extern "C" int h3_gpu_token_pool_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                                      const h3_gpu_tensor *input,
+                                      size_t input_offset,
+                                      h3_gpu_tensor *original,
+                                      size_t original_offset,
+                                      h3_gpu_tensor *baseline,
+                                      size_t baseline_offset,
+                                      const h3_gpu_tensor *baseline_indices,
+                                      const h3_gpu_tensor *pairs,
+                                      uint32_t input_rows, uint32_t rows,
+                                      uint32_t baseline_rows, uint32_t width) {
+    hk_token_args a;
+    if (!hk_pool_setup(gpu, a, output, input, input_offset, original,
+                       original_offset, baseline, baseline_offset,
+                       baseline_indices, pairs, input_rows, rows,
+                       baseline_rows, width, "token pool"))
+        return 0;
+    return hk_token_launch(gpu, false, false, a, "token_pool");
+}
+
+extern "C" int h3_gpu_token_pool_adaln_bf16(
+    h3_gpu *gpu, h3_gpu_tensor *residual, h3_gpu_tensor *output,
+    const h3_gpu_tensor *input, size_t input_offset, h3_gpu_tensor *original,
+    size_t original_offset, h3_gpu_tensor *baseline, size_t baseline_offset,
+    const h3_gpu_tensor *baseline_indices, const h3_gpu_tensor *pairs,
+    const h3_gpu_tensor *norm_weight, const h3_gpu_tensor *modulation,
+    const h3_gpu_tensor *row_map, uint32_t input_rows, uint32_t rows,
+    uint32_t baseline_rows, uint32_t width, uint32_t slots,
+    uint32_t shift_slot, uint32_t scale_slot, float epsilon) {
+    hk_token_args a;
+    if (!hk_pool_setup(gpu, a, residual, input, input_offset, original,
+                       original_offset, baseline, baseline_offset,
+                       baseline_indices, pairs, input_rows, rows,
+                       baseline_rows, width, "fused token pool") ||
+        !hk_adaln_setup(gpu, a, output, norm_weight, modulation, row_map,
+                        rows, width, slots, shift_slot, scale_slot, epsilon,
+                        "fused token pool"))
+        return 0;
+    return hk_token_launch(gpu, false, true, a, "token_pool_adaln");
+}
+
+/* Shared validation of the expand ops (reference h3_cuda_dit.cu:923-1074). */
+static int hk_expand_setup(h3_gpu *gpu, hk_token_args &a,
+                           h3_gpu_tensor *output,
+                           const h3_gpu_tensor *original,
+                           size_t original_offset,
+                           const h3_gpu_tensor *reduced,
+                           const h3_gpu_tensor *baseline,
+                           size_t baseline_offset,
+                           const h3_gpu_tensor *baseline_indices,
+                           const h3_gpu_tensor *parents, uint32_t rows,
+                           uint32_t reduced_rows, uint32_t baseline_rows,
+                           uint32_t width, uint32_t exact_prefix_rows,
+                           float update_scale, const char *what) {
+    const size_t elements = (size_t)rows * width;
+    const size_t reduced_elements = (size_t)reduced_rows * width;
+    const size_t baseline_elements = (size_t)baseline_rows * width;
+    if (!rows || !reduced_rows || reduced_rows > rows ||
+        baseline_rows > reduced_rows || !width ||
+        exact_prefix_rows > reduced_rows || elements > UINT32_MAX ||
+        reduced_elements > UINT32_MAX || original_offset > UINT32_MAX ||
+        elements > UINT32_MAX - original_offset ||
+        baseline_offset > UINT32_MAX ||
+        baseline_elements > UINT32_MAX - baseline_offset)
+        return hk_fail(gpu, "%s shape is out of range", what);
+    if (width % 8 || width > 256 * 8 * HK_TOKEN_CHUNKS)
+        return hk_fail(gpu, "%s width must be a multiple of 8 up to %d", what,
+                       256 * 8 * HK_TOKEN_CHUNKS);
+    if (!hk_token_fits(original, original_offset, elements, H3_GPU_BF16))
+        return hk_fail(gpu, "%s original tensor is too small", what);
+    if (!hk_token_fits(baseline, baseline_offset, baseline_elements,
+                       H3_GPU_BF16))
+        return hk_fail(gpu, "%s baseline tensor is too small", what);
+    if (!hk_token_fits(reduced, 0, reduced_elements, H3_GPU_BF16))
+        return hk_fail(gpu, "%s reduced tensor is too small", what);
+    if (!HK_REQ_BF16(output, elements, "token expand output") ||
+        !HK_REQ_U32(baseline_indices, reduced_rows,
+                    "token expand baseline indices") ||
+        !HK_REQ_U32(parents, rows, "token expand parents") ||
+        !hk_require_active(gpu))
+        return 0;
+    memset(&a, 0, sizeof(a));
+    a.input = HK_CBF16(reduced);
+    a.original = (uint16_t *)HK_CBF16(original);
+    a.baseline = (uint16_t *)HK_CBF16(baseline);
+    a.baseline_indices = HK_CU32(baseline_indices);
+    a.index = HK_CU32(parents);
+    a.residual = HK_BF16(output);
+    a.input_bytes = (uint32_t)reduced->bytes;
+    a.original_bytes = (uint32_t)original->bytes;
+    a.baseline_bytes = (uint32_t)baseline->bytes;
+    a.index_bytes = (uint32_t)parents->bytes;
+    a.baseline_index_bytes = (uint32_t)baseline_indices->bytes;
+    a.original_offset = (uint32_t)original_offset;
+    a.baseline_offset = (uint32_t)baseline_offset;
+    a.rows = rows;
+    a.width = width;
+    a.exact_prefix_rows = exact_prefix_rows;
+    a.update_scale = update_scale;
+    return 1;
+}
+
+extern "C" int h3_gpu_token_expand_delta_bf16(
+    h3_gpu *gpu, h3_gpu_tensor *output, const h3_gpu_tensor *original,
+    size_t original_offset, const h3_gpu_tensor *reduced,
+    const h3_gpu_tensor *baseline, size_t baseline_offset,
+    const h3_gpu_tensor *baseline_indices, const h3_gpu_tensor *parents,
+    uint32_t rows, uint32_t reduced_rows, uint32_t baseline_rows,
+    uint32_t width, uint32_t exact_prefix_rows, float update_scale) {
+    hk_token_args a;
+    if (!hk_expand_setup(gpu, a, output, original, original_offset, reduced,
+                         baseline, baseline_offset, baseline_indices, parents,
+                         rows, reduced_rows, baseline_rows, width,
+                         exact_prefix_rows, update_scale, "token expand"))
+        return 0;
+    return hk_token_launch(gpu, true, false, a, "token_expand");
+}
+
+extern "C" int h3_gpu_token_expand_adaln_bf16(
+    h3_gpu *gpu, h3_gpu_tensor *residual, h3_gpu_tensor *output,
+    const h3_gpu_tensor *original, size_t original_offset,
+    const h3_gpu_tensor *reduced, const h3_gpu_tensor *baseline,
+    size_t baseline_offset, const h3_gpu_tensor *baseline_indices,
+    const h3_gpu_tensor *parents, const h3_gpu_tensor *norm_weight,
+    const h3_gpu_tensor *modulation, const h3_gpu_tensor *row_map,
+    uint32_t rows, uint32_t reduced_rows, uint32_t baseline_rows,
+    uint32_t width, uint32_t exact_prefix_rows, float update_scale,
+    uint32_t slots, uint32_t shift_slot, uint32_t scale_slot, float epsilon) {
+    hk_token_args a;
+    if (!hk_expand_setup(gpu, a, residual, original, original_offset, reduced,
+                         baseline, baseline_offset, baseline_indices, parents,
+                         rows, reduced_rows, baseline_rows, width,
+                         exact_prefix_rows, update_scale,
+                         "fused token adaLN") ||
+        !hk_adaln_setup(gpu, a, output, norm_weight, modulation, row_map,
+                        rows, width, slots, shift_slot, scale_slot, epsilon,
+                        "fused token adaLN"))
+        return 0;
+    return hk_token_launch(gpu, true, true, a, "token_expand_adaln");
+}

@@ -70,13 +70,3 @@ HK_STUB(h3_gpu_rope_text_bf16, T *, T *, CT *, CT *, uint32_t, uint32_t,
         uint32_t, uint32_t)
 HK_STUB(h3_gpu_gqa_causal_bf16, T *, CT *, CT *, CT *, uint32_t, uint32_t,
         uint32_t, uint32_t, float)
-HK_STUB(h3_gpu_token_pool_bf16, T *, CT *, size_t, T *, size_t, T *, size_t,
-        CT *, CT *, uint32_t, uint32_t, uint32_t, uint32_t)
-HK_STUB(h3_gpu_token_pool_adaln_bf16, T *, T *, CT *, size_t, T *, size_t,
-        T *, size_t, CT *, CT *, CT *, CT *, CT *, uint32_t, uint32_t,
-        uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, float)
-HK_STUB(h3_gpu_token_expand_delta_bf16, T *, CT *, size_t, CT *, CT *, size_t,
-        CT *, CT *, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, float)
-HK_STUB(h3_gpu_token_expand_adaln_bf16, T *, T *, CT *, size_t, CT *, CT *,
-        size_t, CT *, CT *, CT *, CT *, CT *, uint32_t, uint32_t, uint32_t,
-        uint32_t, uint32_t, float, uint32_t, uint32_t, uint32_t, float)

@@ -197,6 +197,19 @@ def lib():
                                          C.c_uint, C.c_uint, C.c_uint, _P,
                                          _P, _SZ]),
         "h3_gpu_sdpa_set_sparse": (_I, [_P, _P, _SZ, _P, _SZ, _U32]),
+        "h3_gpu_token_pool_bf16": (_I, [_P, _P, _P, _SZ, _P, _SZ, _P, _SZ,
+                                        _P, _P, _U32, _U32, _U32, _U32]),
+        "h3_gpu_token_pool_adaln_bf16": (_I, [_P, _P, _P, _P, _SZ, _P, _SZ,
+                                              _P, _SZ, _P, _P, _P, _P, _P,
+                                              _U32, _U32, _U32, _U32, _U32,
+                                              _U32, _U32, _F]),
+        "h3_gpu_token_expand_delta_bf16": (_I, [_P, _P, _P, _SZ, _P, _P, _SZ,
+                                                _P, _P, _U32, _U32, _U32,
+                                                _U32, _U32, _F]),
+        "h3_gpu_token_expand_adaln_bf16": (_I, [_P, _P, _P, _P, _SZ, _P, _P,
+                                                _SZ, _P, _P, _P, _P, _P, _U32,
+                                                _U32, _U32, _U32, _U32, _F,
+                                                _U32, _U32, _U32, _F]),
         "h3hip_dit_sampler_rows": (None, [_P, C.POINTER(_U32),
                                           C.POINTER(_U32), C.POINTER(_U32),
                                           C.POINTER(_U32)]),

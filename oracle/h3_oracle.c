@@ -459,6 +459,56 @@ void orc_sdpa_sparse(const bf16 *q, const bf16 *k, const bf16 *v, bf16 *out,
     }
 }
 
+/* Token reduction (reference h3_cuda_dit.cu:336-360, 410-439): pool rows
+ * pair.x / pair.y of the grid into one reduced row (their f32 mean rounded
+ * to bf16, or the single row when they coincide), snapshotting the source
+ * rows into original and the pooled row into baseline[baseline_index]. */
+void orc_token_pool(const bf16 *input, const uint32_t *pairs, bf16 *output,
+                    bf16 *baseline, const uint32_t *baseline_indices,
+                    bf16 *original, size_t rows, size_t width) {
+    for (size_t r = 0; r < rows; r++) {
+        const uint32_t x = pairs[2 * r], y = pairs[2 * r + 1];
+        for (size_t c = 0; c < width; c++) {
+            const bf16 first = input[(size_t)x * width + c];
+            original[(size_t)x * width + c] = first;
+            bf16 pooled = first;
+            if (x != y) {
+                const bf16 second = input[(size_t)y * width + c];
+                original[(size_t)y * width + c] = second;
+                pooled = f2b((b2f(first) + b2f(second)) * 0.5f);
+            }
+            output[r * width + c] = pooled;
+            if (baseline_indices[r] != 0xffffffffu)
+                baseline[(size_t)baseline_indices[r] * width + c] = pooled;
+        }
+    }
+}
+
+/* Token expansion (reference h3_cuda_dit.cu:441-470): full row r takes its
+ * parent's reduced row directly (exact prefix, or no baseline), else
+ * bf16(original + scale * (reduced - baseline)) with the FMA the kernel's
+ * a * b + c contracts to. */
+void orc_token_expand(const bf16 *original, const bf16 *reduced,
+                      const bf16 *baseline, const uint32_t *baseline_indices,
+                      const uint32_t *parents, bf16 *output, size_t rows,
+                      size_t width, size_t exact_prefix_rows,
+                      float update_scale) {
+    for (size_t r = 0; r < rows; r++) {
+        const uint32_t parent = parents[r];
+        const uint32_t b = baseline_indices[parent];
+        for (size_t c = 0; c < width; c++) {
+            const bf16 red = reduced[(size_t)parent * width + c];
+            if (r < exact_prefix_rows || b == 0xffffffffu) {
+                output[r * width + c] = red;
+                continue;
+            }
+            const float update = b2f(red) - b2f(baseline[(size_t)b * width + c]);
+            output[r * width + c] =
+                f2b(fmaf(update_scale, update, b2f(original[r * width + c])));
+        }
+    }
+}
+
 /* ------------------------------------------------------- elementwise */
 
 static inline float silu(float x) { return x / (1.0f + expf(-x)); }

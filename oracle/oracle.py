@@ -36,6 +36,8 @@ def lib():
         sig = {
             "orc_linear_bf16": [_P, _P, _P, _P, _SZ, _SZ, _SZ],
             "orc_linear_f32": [_P, _P, _P, _P, _SZ, _SZ, _SZ],
+            "orc_token_pool": [_P, _P, _P, _P, _P, _P, _SZ, _SZ],
+            "orc_token_expand": [_P, _P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _F],
             "orc_sdpa_sparse": [_P, _P, _P, _P, _SZ, _SZ, _SZ, _F, C.c_int,
                                 C.c_int, _P, _P],
             "orc_patch_linear": [_P, _P, _P, _P, _P, _SZ, _SZ, _SZ],
@@ -221,6 +223,35 @@ def sdpa_sparse(q, k, v, rows, heads, hd, scale, ptr, idx,
     lib().orc_sdpa_sparse(_p(_u16(q)), _p(_u16(k)), _p(_u16(v)), _p(out),
                           rows, heads, hd, scale, int(head_major),
                           int(round_p), _p(p), _p(i))
+    return out
+
+
+def token_pool(inp, pairs, baseline_indices, input_rows, rows,
+               baseline_rows, width):
+    """h3_cuda_dit.cu:336-360; returns (output, original, baseline).
+    original / baseline start as zeros where nothing is written."""
+    out = np.zeros(rows * width, np.uint16)
+    original = np.zeros(input_rows * width, np.uint16)
+    baseline = np.zeros(max(baseline_rows, 1) * width, np.uint16)
+    lib().orc_token_pool(_p(_u16(inp)),
+                         _p(np.ascontiguousarray(pairs, np.uint32)), _p(out),
+                         _p(baseline),
+                         _p(np.ascontiguousarray(baseline_indices, np.uint32)),
+                         _p(original), rows, width)
+    return out, original, baseline
+
+
+def token_expand(original, reduced, baseline, baseline_indices, parents,
+                 rows, width, exact_prefix_rows, update_scale):
+    """h3_cuda_dit.cu:441-470."""
+    out = np.empty(rows * width, np.uint16)
+    lib().orc_token_expand(_p(_u16(original)), _p(_u16(reduced)),
+                           _p(_u16(baseline)),
+                           _p(np.ascontiguousarray(baseline_indices,
+                                                   np.uint32)),
+                           _p(np.ascontiguousarray(parents, np.uint32)),
+                           _p(out), rows, width, exact_prefix_rows,
+                           update_scale)
     return out
 
 

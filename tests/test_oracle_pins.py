@@ -456,3 +456,38 @@ def test_bf16_rounding_is_rne():
     got = to_f32(b(vals))
     assert got[0] == 1.0 and got[1] == 1 + 2 ** -6 and got[2] == -1.0
     assert bf16_ulp_distance(b(vals[3:4]), b(np.float32(1e-40))) == 0
+
+
+def test_token_pool_expand_pins():
+    """Token reduction oracle (h3_cuda_dit.cu:336-470): a singleton pair
+    copies its row; a pair of small integers pools to their exact mean;
+    expanding an unchanged stack (reduced == baseline, scale 1) restores the
+    original grid bit for bit; scale 0 returns the original rows; exact
+    prefix rows take the reduced row."""
+    width, input_rows = 8, 5
+    x = rng.integers(-8, 9, (input_rows, width)).astype(np.float32) * 2
+    pairs = np.array([0, 3, 1, 1, 2, 4], np.uint32)        # rows 0..2
+    bidx = np.array([0, 0xFFFFFFFF, 1], np.uint32)
+    out, orig, base = oracle.token_pool(b(x), pairs, bidx, input_rows, 3, 2,
+                                        width)
+    o = f64(out).reshape(3, width)
+    np.testing.assert_array_equal(o[0], (x[0] + x[3]) / 2)
+    np.testing.assert_array_equal(o[1], x[1])
+    np.testing.assert_array_equal(o[2], (x[2] + x[4]) / 2)
+    np.testing.assert_array_equal(f64(orig).reshape(input_rows, width), x)
+    np.testing.assert_array_equal(f64(base).reshape(2, width),
+                                  o[[0, 2]])
+    parents = np.array([0, 1, 2, 0, 2], np.uint32)
+    same = oracle.token_expand(orig, out, base, bidx, parents, input_rows,
+                               width, 0, 1.0)
+    # rows with a baseline return the original; row 1 has none -> reduced
+    want = f64(orig).reshape(input_rows, width).copy()
+    want[1] = o[1]
+    np.testing.assert_array_equal(f64(same).reshape(input_rows, width), want)
+    moved = b(f64(out) + 1.0)
+    zero = oracle.token_expand(orig, moved, base, bidx, parents, input_rows,
+                               width, 2, 0.0)
+    z = f64(zero).reshape(input_rows, width)
+    np.testing.assert_array_equal(z[0], f64(moved).reshape(3, width)[0])
+    np.testing.assert_array_equal(z[2:], want[2:] * 0 +
+                                  f64(orig).reshape(input_rows, width)[2:])
