@@ -59,6 +59,8 @@ struct h3_gpu {
      * 128-row query blocks of 64-row key tiles, each list sorted */
     uint32_t *sparse_ptr, *sparse_idx; /* device */
     uint32_t sparse_rows;
+    /* file loader: pinned staging slots, copy stream, serialising lock */
+    struct hk_loader *loader;
 };
 
 /* stats kinds, mirroring the reference counters (h3_cuda_internal.h:142-160) */

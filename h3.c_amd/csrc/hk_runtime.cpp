@@ -21,7 +21,9 @@
 #include <time.h>
 #include <unistd.h>
 
+#include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 double hk_now(void) {
@@ -316,6 +318,9 @@ static int hk_env_flag(const char *name) {
     return value && *value && strcmp(value, "0") != 0;
 }
 
+static bool hk_loader_new(struct h3_gpu *gpu);
+static void hk_loader_free(struct h3_gpu *gpu);
+
 extern "C" h3_gpu *h3_gpu_create(const char *shader_source_path,
                                  char *error, size_t error_size) {
     (void)shader_source_path; /* kernels are compiled into the library */
@@ -354,6 +359,12 @@ extern "C" h3_gpu *h3_gpu_create(const char *shader_source_path,
     if (gpu->num_cus <= 0) gpu->num_cus = 256;
     gpu->reference_kernels = hk_env_flag("H3_HIP_REFERENCE");
     gpu->profile_mark_wall = hk_now();
+    if (!hk_loader_new(gpu)) {
+        if (error && error_size) snprintf(error, error_size, "out of memory");
+        (void)hipStreamDestroy(gpu->stream);
+        free(gpu);
+        return NULL;
+    }
     return gpu;
 }
 
@@ -375,6 +386,7 @@ extern "C" void h3_gpu_free(h3_gpu *gpu) {
     if (gpu->workspace) (void)hipFree(gpu->workspace);
     if (gpu->sparse_ptr) (void)hipFree(gpu->sparse_ptr);
     if (gpu->sparse_idx) (void)hipFree(gpu->sparse_idx);
+    hk_loader_free(gpu);
     if (gpu->timing) {
         for (auto &launch : gpu->timing->launches) {
             (void)hipEventDestroy(launch.start);
@@ -554,31 +566,234 @@ extern "C" h3_gpu_tensor *h3_gpu_tensor_from_u32(h3_gpu *gpu,
     return hk_tensor_from(gpu, values, n, H3_GPU_U32);
 }
 
-/* Read `bytes` from path at offset into host memory (whole-file pread loop). */
-static int hk_read_file(const char *path, uint64_t offset, void *host,
-                        size_t bytes, char *error, size_t error_size) {
-    int fd = open(path, O_RDONLY);
-    if (fd < 0) {
-        if (error && error_size)
-            snprintf(error, error_size, "cannot open %s: %s", path,
-                     strerror(errno));
-        return 0;
+/* ---- file payloads -> HBM (reference h3_gpu_cuda.cu:426-703) ------------
+ * A pipelined loader instead of the reference's read-all-then-copy: the
+ * 4 KiB-aligned superset of the byte range is cut into 16 MiB chunks;
+ * HK_LOAD_THREADS readers each pread their chunks (O_DIRECT when the file
+ * system allows it, else buffered) into their own two pinned staging slots,
+ * and as each chunk lands its payload part is copied to the device on a
+ * copy stream while the next chunk is being read.  The kernel cannot pin
+ * pages of the driver's pinned mapping for a direct read (EFAULT), so
+ * O_DIRECT reads land in a per-thread aligned bounce buffer and the payload
+ * is copied on into the pinned slot; buffered reads go straight there.  Disk reads and PCIe
+ * transfers overlap, and staging stays bounded at 2 x threads x 16 MiB
+ * whatever the tensor size.  A slot is reused only after the copy out of it
+ * has completed (an event per slot). */
+enum { HK_LOAD_THREADS = 8, HK_LOAD_SLOTS = 2 * HK_LOAD_THREADS };
+static const size_t HK_LOAD_CHUNK = (size_t)16 << 20;
+static const size_t HK_LOAD_ALIGN = 4096;
+
+struct hk_loader {
+    std::mutex lock;
+    unsigned char *slots[HK_LOAD_SLOTS];
+    hipEvent_t done[HK_LOAD_SLOTS];
+    hipEvent_t after; /* compute-stream work queued before the load */
+    unsigned char *bounce[HK_LOAD_THREADS]; /* aligned pageable, O_DIRECT */
+    bool pending[HK_LOAD_SLOTS];
+    hipStream_t copy;
+    bool ready;
+};
+
+static bool hk_loader_new(struct h3_gpu *gpu) {
+    gpu->loader = new (std::nothrow) hk_loader();
+    return gpu->loader != NULL;
+}
+
+/* staging and the copy stream are made on the first load; caller holds the
+ * loader lock */
+static bool hk_loader_init(struct h3_gpu *gpu) {
+    hk_loader *l = gpu->loader;
+    if (l->ready) return true;
+    /* each resource is made once: a failed set-up resumes where it stopped */
+    bool ok = (l->copy || hipStreamCreateWithFlags(&l->copy,
+                                                   hipStreamNonBlocking) ==
+                              hipSuccess) &&
+              (l->after || hipEventCreateWithFlags(&l->after,
+                                                   hipEventDisableTiming) ==
+                               hipSuccess);
+    for (int i = 0; ok && i < HK_LOAD_SLOTS; i++) {
+        /* hipHostMalloc memory is page aligned, as O_DIRECT needs */
+        void *p = l->slots[i];
+        ok = (p || hipHostMalloc(&p, HK_LOAD_CHUNK, hipHostMallocDefault) ==
+                       hipSuccess) &&
+             (l->done[i] || hipEventCreateWithFlags(&l->done[i],
+                                                    hipEventDisableTiming) ==
+                                hipSuccess);
+        if (p) l->slots[i] = (unsigned char *)p;
+        l->pending[i] = false;
     }
+    if (!ok) (void)hipGetLastError();
+    l->ready = ok;
+    return ok;
+}
+
+static void hk_loader_free(struct h3_gpu *gpu) {
+    hk_loader *l = gpu->loader;
+    if (!l) return;
+    if (l->copy) (void)hipStreamSynchronize(l->copy);
+    for (int i = 0; i < HK_LOAD_SLOTS; i++) {
+        if (l->slots[i]) (void)hipHostFree(l->slots[i]);
+        if (l->done[i]) (void)hipEventDestroy(l->done[i]);
+    }
+    for (int t = 0; t < HK_LOAD_THREADS; t++) free(l->bounce[t]);
+    if (l->after) (void)hipEventDestroy(l->after);
+    if (l->copy) (void)hipStreamDestroy(l->copy);
+    delete l;
+    gpu->loader = NULL;
+}
+
+/* pread [offset, +bytes) fully, or until end of file once `need` bytes are
+ * in: returns 0, an errno, or -1 for a file that ends early */
+static int hk_pread_all(int fd, unsigned char *dst, uint64_t offset,
+                        size_t bytes, size_t need) {
     size_t done = 0;
     while (done < bytes) {
-        ssize_t got = pread(fd, (char *)host + done, bytes - done,
+        ssize_t got = pread(fd, dst + done, bytes - done,
                             (off_t)(offset + done));
-        if (got <= 0) {
-            if (got < 0 && errno == EINTR) continue;
-            if (error && error_size)
-                snprintf(error, error_size, "short read from %s", path);
-            close(fd);
-            return 0;
-        }
+        if (got < 0 && errno == EINTR) continue;
+        if (got < 0) return errno;
+        if (got == 0) return done >= need ? 0 : -1;
         done += (size_t)got;
     }
+    return 0;
+}
+
+/* Copy file bytes [offset, +bytes) to device memory `dst`.  Must hold the
+ * loader lock.  Returns 1, or 0 with the message in error. */
+static int hk_load_range(struct h3_gpu *gpu, const char *path,
+                         uint64_t offset, void *dst, size_t bytes,
+                         bool try_direct, char *error, size_t error_size) {
+    hk_loader *l = gpu->loader;
+    if (!bytes) return 1;
+    int fd = try_direct ? open(path, O_RDONLY | O_CLOEXEC | O_DIRECT) : -1;
+    bool direct = fd >= 0;
+    if (!direct) fd = open(path, O_RDONLY | O_CLOEXEC);
+    if (fd < 0) {
+        snprintf(error, error_size, "cannot open %s: %s", path,
+                 strerror(errno));
+        return 0;
+    }
+    const uint64_t end = offset + bytes;
+    const uint64_t span0 = direct ? offset & ~(uint64_t)(HK_LOAD_ALIGN - 1)
+                                  : offset;
+    const uint64_t span1 = direct ? (end + HK_LOAD_ALIGN - 1) &
+                                        ~(uint64_t)(HK_LOAD_ALIGN - 1)
+                                  : end;
+    const size_t chunks = (size_t)((span1 - span0 + HK_LOAD_CHUNK - 1) /
+                                   HK_LOAD_CHUNK);
+    std::vector<int> status(HK_LOAD_THREADS, 0);
+    std::vector<std::thread> readers;
+    auto reader = [&](int t) {
+        for (size_t c = (size_t)t; c < chunks; c += HK_LOAD_THREADS) {
+            const int slot = (int)(c % HK_LOAD_SLOTS);
+            if (l->pending[slot]) {
+                if (hipEventSynchronize(l->done[slot]) != hipSuccess) {
+                    status[t] = EIO;
+                    return;
+                }
+                l->pending[slot] = false;
+            }
+            const uint64_t c0 = span0 + (uint64_t)c * HK_LOAD_CHUNK;
+            const uint64_t c1 = c0 + HK_LOAD_CHUNK < span1
+                ? c0 + HK_LOAD_CHUNK : span1;
+            const uint64_t p0 = c0 > offset ? c0 : offset;
+            const uint64_t p1 = c1 < end ? c1 : end;
+            unsigned char *land = l->slots[slot];
+            if (direct) {
+                if (!l->bounce[t]) {
+                    void *p = NULL;
+                    if (posix_memalign(&p, HK_LOAD_ALIGN, HK_LOAD_CHUNK)) {
+                        status[t] = ENOMEM;
+                        return;
+                    }
+                    l->bounce[t] = (unsigned char *)p;
+                }
+                land = l->bounce[t];
+            }
+            int rc = hk_pread_all(fd, land, c0, (size_t)(c1 - c0),
+                                  (size_t)(p1 - c0));
+            if (rc) {
+                status[t] = rc;
+                return;
+            }
+            if (direct)
+                memcpy(l->slots[slot] + (p0 - c0), land + (p0 - c0),
+                       (size_t)(p1 - p0));
+            if (hipMemcpyAsync((unsigned char *)dst + (p0 - offset),
+                               l->slots[slot] + (p0 - c0), (size_t)(p1 - p0),
+                               hipMemcpyHostToDevice, l->copy) != hipSuccess ||
+                hipEventRecord(l->done[slot], l->copy) != hipSuccess) {
+                status[t] = EIO;
+                return;
+            }
+            l->pending[slot] = true;
+        }
+    };
+    const int threads = chunks < HK_LOAD_THREADS ? (int)chunks
+                                                 : HK_LOAD_THREADS;
+    for (int t = 1; t < threads; t++) {
+        try {
+            readers.emplace_back(reader, t);
+        } catch (...) {
+            status[t] = -2; /* could not start: read inline below */
+        }
+    }
+    reader(0);
+    for (int t = 1; t < threads; t++)
+        if (status[t] == -2) {
+            status[t] = 0;
+            reader(t);
+        }
+    for (auto &r : readers) r.join();
     close(fd);
+    hipError_t sync = hipStreamSynchronize(l->copy);
+    for (int i = 0; i < HK_LOAD_SLOTS; i++) l->pending[i] = false;
+    for (int t = 0; t < threads; t++) {
+        if (!status[t]) continue;
+        if (status[t] == EINVAL && direct) {
+            /* the file system refused O_DIRECT reads: buffered retry */
+            return hk_load_range(gpu, path, offset, dst, bytes, false, error,
+                                 error_size);
+        }
+        snprintf(error, error_size, "cannot read %s: %s", path,
+                 status[t] > 0 ? strerror(status[t])
+                               : "unexpected end of file");
+        return 0;
+    }
+    if (sync != hipSuccess) {
+        snprintf(error, error_size, "file upload failed: %s",
+                 hipGetErrorString(sync));
+        return 0;
+    }
     return 1;
+}
+
+static int hk_load_into(struct h3_gpu *gpu, const char *path, uint64_t offset,
+                        void *dst, size_t bytes, char *error,
+                        size_t error_size) {
+    if (!path || !*path || offset > (uint64_t)INT64_MAX ||
+        (uint64_t)bytes > (uint64_t)INT64_MAX - offset) {
+        snprintf(error, error_size, "invalid file range");
+        return 0;
+    }
+    std::lock_guard<std::mutex> guard(gpu->loader->lock);
+    if (!hk_loader_init(gpu)) {
+        snprintf(error, error_size, "cannot set up pinned staging");
+        return 0;
+    }
+    /* destination memory may be a recycled buffer that work already queued
+     * on the compute stream still touches: order the copies after it */
+    if (hipEventRecord(gpu->loader->after, gpu->stream) != hipSuccess ||
+        hipStreamWaitEvent(gpu->loader->copy, gpu->loader->after, 0) !=
+            hipSuccess) {
+        snprintf(error, error_size, "device error before file load");
+        return 0;
+    }
+    /* H3_HIP_DIRECT_IO=0 forces buffered reads */
+    const char *env = getenv("H3_HIP_DIRECT_IO");
+    const bool direct = !(env && strcmp(env, "0") == 0);
+    return hk_load_range(gpu, path, offset, dst, bytes, direct, error,
+                         error_size);
 }
 
 static h3_gpu_tensor *hk_tensor_load(struct h3_gpu *gpu, const char *path,
@@ -587,18 +802,9 @@ static h3_gpu_tensor *hk_tensor_load(struct h3_gpu *gpu, const char *path,
     if (!gpu || !path) return NULL;
     h3_gpu_tensor *tensor = hk_tensor_new(gpu, elements, dtype);
     if (!tensor) return NULL;
-    void *host = NULL;
-    if (hipHostMalloc(&host, tensor->bytes ? tensor->bytes : 1,
-                      hipHostMallocDefault) != hipSuccess) {
-        (void)hipGetLastError();
-        host = NULL;
-    }
-    int ok = host && hk_read_file(path, offset, host, tensor->bytes,
-                                  gpu->error, sizeof(gpu->error)) &&
-             hk_upload(gpu, tensor->data, host, tensor->bytes);
-    if (host) (void)hipHostFree(host);
-    if (!ok) {
-        if (!host) hk_fail(gpu, "cannot allocate pinned staging");
+    if (!hk_load_into(gpu, path, offset, tensor->data,
+                      elements * hk_item_size(dtype), gpu->error,
+                      sizeof(gpu->error))) {
         h3_gpu_tensor_free(tensor);
         return NULL;
     }
@@ -617,36 +823,26 @@ extern "C" h3_gpu_tensor *h3_gpu_tensor_load_f32(h3_gpu *gpu,
     return hk_tensor_load(gpu, path, offset, n, H3_GPU_F32);
 }
 
+/* May run on an I/O thread while the calling thread keeps issuing work
+ * (reference h3_gpu.h:67-78): the loader lock serialises loads, and the
+ * copy stream never touches the context's compute stream. */
 extern "C" int h3_gpu_tensor_read_file_bf16(h3_gpu_tensor *tensor,
                                             const char *path,
                                             uint64_t offset, size_t elements,
                                             char *error, size_t error_size) {
-    if (!tensor || tensor->dtype != H3_GPU_BF16 ||
-        elements > tensor->elements) {
-        if (error && error_size)
-            snprintf(error, error_size, "invalid BF16 file read target");
+    char local[256];
+    if (!error || !error_size) {
+        error = local;
+        error_size = sizeof(local);
+    }
+    error[0] = '\0';
+    if (!tensor || !tensor->owner || tensor->dtype != H3_GPU_BF16 ||
+        elements != tensor->elements) {
+        snprintf(error, error_size, "invalid BF16 file read request");
         return 0;
     }
-    size_t bytes = elements * 2;
-    void *host = malloc(bytes ? bytes : 1);
-    if (!host) {
-        if (error && error_size) snprintf(error, error_size, "out of memory");
-        return 0;
-    }
-    int ok = hk_read_file(path, offset, host, bytes, error, error_size);
-    /* may run on an I/O thread: synchronous copy on the null stream */
-    if (ok && bytes) {
-        hipError_t status = hipMemcpy(tensor->data, host, bytes,
-                                      hipMemcpyHostToDevice);
-        if (status != hipSuccess) {
-            if (error && error_size)
-                snprintf(error, error_size, "upload failed: %s",
-                         hipGetErrorString(status));
-            ok = 0;
-        }
-    }
-    free(host);
-    return ok;
+    return hk_load_into(tensor->owner, path, offset, tensor->data,
+                        elements * 2, error, error_size);
 }
 
 extern "C" int h3_gpu_tensor_stream_file_bf16(h3_gpu_tensor *tensor,

@@ -196,6 +196,12 @@ def lib():
         "h3hip_sparse_mask": (C.c_long, [C.POINTER(Layout), C.c_uint,
                                          C.c_uint, C.c_uint, C.c_uint, _P,
                                          _P, _SZ]),
+        "h3_gpu_tensor_load_bf16": (_P, [_P, C.c_char_p, C.c_uint64, _SZ]),
+        "h3_gpu_tensor_load_f32": (_P, [_P, C.c_char_p, C.c_uint64, _SZ]),
+        "h3_gpu_tensor_read_file_bf16": (_I, [_P, C.c_char_p, C.c_uint64,
+                                              _SZ, C.c_char_p, _SZ]),
+        "h3_gpu_tensor_stream_file_bf16": (_I, [_P, C.c_char_p, C.c_uint64,
+                                                _SZ, C.c_char_p, _SZ]),
         "h3_gpu_sdpa_set_sparse": (_I, [_P, _P, _SZ, _P, _SZ, _U32]),
         "h3_gpu_token_pool_bf16": (_I, [_P, _P, _P, _SZ, _P, _SZ, _P, _SZ,
                                         _P, _P, _U32, _U32, _U32, _U32]),
@@ -349,6 +355,23 @@ class Gpu:
         self.check(t, "f32 alloc")
         self._owned.append(t)
         return t
+
+    def load(self, path, offset, n, dtype="bf16"):
+        """h3_gpu_tensor_load_{bf16,f32}: file bytes -> a new tensor."""
+        fn = (self.L.h3_gpu_tensor_load_bf16 if dtype == "bf16"
+              else self.L.h3_gpu_tensor_load_f32)
+        t = fn(self.h, str(path).encode(), offset, n)
+        self.check(t, f"{dtype} file load")
+        self._owned.append(t)
+        return t
+
+    def read_file(self, t, path, offset, n, stream=False):
+        """h3_gpu_tensor_{read,stream}_file_bf16 into an existing tensor."""
+        err = C.create_string_buffer(512)
+        fn = (self.L.h3_gpu_tensor_stream_file_bf16 if stream
+              else self.L.h3_gpu_tensor_read_file_bf16)
+        if not fn(t, str(path).encode(), offset, n, err, 512):
+            raise RuntimeError("file read failed: " + err.value.decode())
 
     def free(self, t):
         if t in self._owned:
@@ -530,3 +553,23 @@ def dit_config(family, hidden, heads, ffn, rows, blocks=1, text_rows=0,
 def block_flops(cfg):
     """FLOPs of one block (host math only, no device needed)."""
     return lib().h3hip_dit_block_flops(C.byref(cfg))
+
+
+def safetensors_index(path):
+    """Tensor name -> (dtype, shape, absolute byte offset, byte count) from a
+    safetensors header: an 8-byte little-endian length, then that many bytes
+    of JSON whose data_offsets are relative to the end of the header (the
+    format h3_weights.c reads)."""
+    import json
+    import struct
+    with open(path, "rb") as f:
+        (n,) = struct.unpack("<Q", f.read(8))
+        header = json.loads(f.read(n))
+    base = 8 + n
+    out = {}
+    for name, info in header.items():
+        if name == "__metadata__":
+            continue
+        a, b = info["data_offsets"]
+        out[name] = (info["dtype"], tuple(info["shape"]), base + a, b - a)
+    return out

@@ -345,3 +345,20 @@ def test_host_euler_literal():
     assert x.tolist() == [2.0, 1.0]
     assert not L.h3hip_euler_velocity_step(h3hip.ptr(x), h3hip.ptr(v), 2,
                                            C.c_float(0.25), C.c_float(0.25))
+
+
+def test_safetensors_index_reads_the_header(tmp_path):
+    """The header walk used to locate tensors in a safetensors file, checked
+    on a file written by the safetensors library itself."""
+    np_st = pytest.importorskip("safetensors.numpy")
+    import h3hip
+    a = np.arange(12, dtype=np.float32).reshape(3, 4)
+    b = np.arange(5, dtype=np.uint16)
+    path = str(tmp_path / "m.safetensors")
+    np_st.save_file({"a": a, "b": b}, path)
+    idx = h3hip.safetensors_index(path)
+    raw = open(path, "rb").read()
+    assert idx["a"][:2] == ("F32", (3, 4)) and idx["b"][:2] == ("U16", (5,))
+    for name, arr in (("a", a), ("b", b)):
+        _, _, off, nbytes = idx[name]
+        assert raw[off:off + nbytes] == arr.tobytes()
