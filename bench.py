@@ -268,6 +268,49 @@ def wan_864x480(gpu, blocks, reps):
         dit.close()
 
 
+def weight_load(size_gib=2.0):
+    """File -> HBM throughput of h3_gpu_tensor_load_bf16 on a freshly
+    written file (so mostly page-cache resident): O_DIRECT and buffered
+    reads, against read-everything-then-upload (h3_gpu_tensor_from_bf16 of
+    an np.fromfile array), the reference's load order."""
+    import shutil
+    import tempfile
+    n = int(size_gib * (1 << 30)) // 2
+    d = tempfile.mkdtemp(prefix=".bench_load_", dir=ROOT)
+    out = {"bytes": 2 * n, "file": "random bytes behind a 4 KiB header"}
+    try:
+        path = os.path.join(d, "weights.bin")
+        with open(path, "wb") as f:
+            f.write(b"\0" * 4096)
+            np.random.default_rng(0).integers(
+                0, 1 << 16, n, dtype=np.uint16).tofile(f)
+        gpu = h3hip.Gpu()
+        try:
+            for mode, env in (("direct", "1"), ("buffered", "0")):
+                os.environ["H3_HIP_DIRECT_IO"] = env
+                best = None
+                for _ in range(3):
+                    t0 = time.perf_counter()
+                    t = gpu.load(path, 4096, n)
+                    dt = time.perf_counter() - t0
+                    gpu.free(t)
+                    best = dt if best is None else min(best, dt)
+                out[mode + "_gb_s"] = round(2 * n / best / 1e9, 2)
+            os.environ.pop("H3_HIP_DIRECT_IO", None)
+            t0 = time.perf_counter()
+            a = np.fromfile(path, dtype=np.uint16, offset=4096)
+            t = gpu.bf16(a)
+            dt = time.perf_counter() - t0
+            gpu.free(t)
+            del a
+            out["read_then_upload_gb_s"] = round(2 * n / dt / 1e9, 2)
+        finally:
+            gpu.close()
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    return out
+
+
 def load_traffic(name):
     """HBM bytes per launch of the dominant kernel, measured offline with two
     rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) and calibrated on a copy
@@ -398,6 +441,9 @@ def main():
         log("H3 real shape: forward + 20-step Euler denoise ...")
         h3_real, denoise = h3_measure(gpu, blocks, max(2, args.steps // 2))
 
+    log("weight file loading ...")
+    loading = weight_load()
+
     base = None
     if not args.no_cpu_baseline:
         log("CPU baseline ...")
@@ -462,6 +508,7 @@ def main():
         "denoise": denoise,
         "attention_sweep": sweep,
         "wan_864x480": wan_big,
+        "weight_load": loading,
         "cpu_baseline": base,
     }
     gpu.close()

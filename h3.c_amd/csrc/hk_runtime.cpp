@@ -568,19 +568,19 @@ extern "C" h3_gpu_tensor *h3_gpu_tensor_from_u32(h3_gpu *gpu,
 
 /* ---- file payloads -> HBM (reference h3_gpu_cuda.cu:426-703) ------------
  * A pipelined loader instead of the reference's read-all-then-copy: the
- * 4 KiB-aligned superset of the byte range is cut into 16 MiB chunks;
- * HK_LOAD_THREADS readers each pread their chunks (O_DIRECT when the file
+ * 4 KiB-aligned superset of the byte range is cut into 8 MiB chunks;
+ * up to HK_LOAD_THREADS readers (H3_HIP_LOAD_THREADS, default 16) each pread their chunks (O_DIRECT when the file
  * system allows it, else buffered) into their own two pinned staging slots,
  * and as each chunk lands its payload part is copied to the device on a
  * copy stream while the next chunk is being read.  The kernel cannot pin
  * pages of the driver's pinned mapping for a direct read (EFAULT), so
  * O_DIRECT reads land in a per-thread aligned bounce buffer and the payload
  * is copied on into the pinned slot; buffered reads go straight there.  Disk reads and PCIe
- * transfers overlap, and staging stays bounded at 2 x threads x 16 MiB
+ * transfers overlap, and staging stays bounded at 2 x 16 x 8 MiB
  * whatever the tensor size.  A slot is reused only after the copy out of it
  * has completed (an event per slot). */
-enum { HK_LOAD_THREADS = 8, HK_LOAD_SLOTS = 2 * HK_LOAD_THREADS };
-static const size_t HK_LOAD_CHUNK = (size_t)16 << 20;
+enum { HK_LOAD_THREADS = 16, HK_LOAD_SLOTS = 2 * HK_LOAD_THREADS };
+static const size_t HK_LOAD_CHUNK = (size_t)8 << 20;
 static const size_t HK_LOAD_ALIGN = 4096;
 
 struct hk_loader {
@@ -662,7 +662,8 @@ static int hk_pread_all(int fd, unsigned char *dst, uint64_t offset,
  * loader lock.  Returns 1, or 0 with the message in error. */
 static int hk_load_range(struct h3_gpu *gpu, const char *path,
                          uint64_t offset, void *dst, size_t bytes,
-                         bool try_direct, char *error, size_t error_size) {
+                         bool try_direct, bool no_reuse, char *error,
+                         size_t error_size) {
     hk_loader *l = gpu->loader;
     if (!bytes) return 1;
     int fd = try_direct ? open(path, O_RDONLY | O_CLOEXEC | O_DIRECT) : -1;
@@ -672,6 +673,14 @@ static int hk_load_range(struct h3_gpu *gpu, const char *path,
         snprintf(error, error_size, "cannot open %s: %s", path,
                  strerror(errno));
         return 0;
+    }
+    if (no_reuse && !direct)
+        (void)posix_fadvise(fd, (off_t)offset, (off_t)bytes,
+                            POSIX_FADV_NOREUSE);
+    int max_threads = HK_LOAD_THREADS;
+    if (const char *env = getenv("H3_HIP_LOAD_THREADS")) {
+        int v = atoi(env);
+        if (v >= 1 && v <= HK_LOAD_THREADS) max_threads = v;
     }
     const uint64_t end = offset + bytes;
     const uint64_t span0 = direct ? offset & ~(uint64_t)(HK_LOAD_ALIGN - 1)
@@ -683,9 +692,13 @@ static int hk_load_range(struct h3_gpu *gpu, const char *path,
                                    HK_LOAD_CHUNK);
     std::vector<int> status(HK_LOAD_THREADS, 0);
     std::vector<std::thread> readers;
+    const int threads = chunks < (size_t)max_threads ? (int)chunks
+                                                     : max_threads;
     auto reader = [&](int t) {
-        for (size_t c = (size_t)t; c < chunks; c += HK_LOAD_THREADS) {
-            const int slot = (int)(c % HK_LOAD_SLOTS);
+        for (size_t c = (size_t)t; c < chunks; c += (size_t)threads) {
+            /* thread t owns slots t and t + HK_LOAD_THREADS */
+            const int slot = t + (int)((c / (size_t)threads) & 1) *
+                                     HK_LOAD_THREADS;
             if (l->pending[slot]) {
                 if (hipEventSynchronize(l->done[slot]) != hipSuccess) {
                     status[t] = EIO;
@@ -729,8 +742,6 @@ static int hk_load_range(struct h3_gpu *gpu, const char *path,
             l->pending[slot] = true;
         }
     };
-    const int threads = chunks < HK_LOAD_THREADS ? (int)chunks
-                                                 : HK_LOAD_THREADS;
     for (int t = 1; t < threads; t++) {
         try {
             readers.emplace_back(reader, t);
@@ -752,8 +763,8 @@ static int hk_load_range(struct h3_gpu *gpu, const char *path,
         if (!status[t]) continue;
         if (status[t] == EINVAL && direct) {
             /* the file system refused O_DIRECT reads: buffered retry */
-            return hk_load_range(gpu, path, offset, dst, bytes, false, error,
-                                 error_size);
+            return hk_load_range(gpu, path, offset, dst, bytes, false,
+                                 no_reuse, error, error_size);
         }
         snprintf(error, error_size, "cannot read %s: %s", path,
                  status[t] > 0 ? strerror(status[t])
@@ -768,9 +779,12 @@ static int hk_load_range(struct h3_gpu *gpu, const char *path,
     return 1;
 }
 
+/* direct: O_DIRECT first (whole-tensor loads, as the reference does);
+ * otherwise buffered reads, with no_reuse asking the page cache not to keep
+ * the payload (the reference's stream variant). */
 static int hk_load_into(struct h3_gpu *gpu, const char *path, uint64_t offset,
-                        void *dst, size_t bytes, char *error,
-                        size_t error_size) {
+                        void *dst, size_t bytes, bool direct, bool no_reuse,
+                        char *error, size_t error_size) {
     if (!path || !*path || offset > (uint64_t)INT64_MAX ||
         (uint64_t)bytes > (uint64_t)INT64_MAX - offset) {
         snprintf(error, error_size, "invalid file range");
@@ -791,9 +805,9 @@ static int hk_load_into(struct h3_gpu *gpu, const char *path, uint64_t offset,
     }
     /* H3_HIP_DIRECT_IO=0 forces buffered reads */
     const char *env = getenv("H3_HIP_DIRECT_IO");
-    const bool direct = !(env && strcmp(env, "0") == 0);
-    return hk_load_range(gpu, path, offset, dst, bytes, direct, error,
-                         error_size);
+    if (env && strcmp(env, "0") == 0) direct = false;
+    return hk_load_range(gpu, path, offset, dst, bytes, direct, no_reuse,
+                         error, error_size);
 }
 
 static h3_gpu_tensor *hk_tensor_load(struct h3_gpu *gpu, const char *path,
@@ -803,8 +817,8 @@ static h3_gpu_tensor *hk_tensor_load(struct h3_gpu *gpu, const char *path,
     h3_gpu_tensor *tensor = hk_tensor_new(gpu, elements, dtype);
     if (!tensor) return NULL;
     if (!hk_load_into(gpu, path, offset, tensor->data,
-                      elements * hk_item_size(dtype), gpu->error,
-                      sizeof(gpu->error))) {
+                      elements * hk_item_size(dtype), true, false,
+                      gpu->error, sizeof(gpu->error))) {
         h3_gpu_tensor_free(tensor);
         return NULL;
     }
@@ -826,10 +840,9 @@ extern "C" h3_gpu_tensor *h3_gpu_tensor_load_f32(h3_gpu *gpu,
 /* May run on an I/O thread while the calling thread keeps issuing work
  * (reference h3_gpu.h:67-78): the loader lock serialises loads, and the
  * copy stream never touches the context's compute stream. */
-extern "C" int h3_gpu_tensor_read_file_bf16(h3_gpu_tensor *tensor,
-                                            const char *path,
-                                            uint64_t offset, size_t elements,
-                                            char *error, size_t error_size) {
+static int hk_read_file(h3_gpu_tensor *tensor, const char *path,
+                        uint64_t offset, size_t elements, bool no_reuse,
+                        char *error, size_t error_size) {
     char local[256];
     if (!error || !error_size) {
         error = local;
@@ -842,7 +855,15 @@ extern "C" int h3_gpu_tensor_read_file_bf16(h3_gpu_tensor *tensor,
         return 0;
     }
     return hk_load_into(tensor->owner, path, offset, tensor->data,
-                        elements * 2, error, error_size);
+                        elements * 2, false, no_reuse, error, error_size);
+}
+
+extern "C" int h3_gpu_tensor_read_file_bf16(h3_gpu_tensor *tensor,
+                                            const char *path,
+                                            uint64_t offset, size_t elements,
+                                            char *error, size_t error_size) {
+    return hk_read_file(tensor, path, offset, elements, false, error,
+                        error_size);
 }
 
 extern "C" int h3_gpu_tensor_stream_file_bf16(h3_gpu_tensor *tensor,
@@ -850,8 +871,8 @@ extern "C" int h3_gpu_tensor_stream_file_bf16(h3_gpu_tensor *tensor,
                                               uint64_t offset,
                                               size_t elements, char *error,
                                               size_t error_size) {
-    return h3_gpu_tensor_read_file_bf16(tensor, path, offset, elements, error,
-                                        error_size);
+    return hk_read_file(tensor, path, offset, elements, true, error,
+                        error_size);
 }
 
 extern "C" void h3_gpu_tensor_free(h3_gpu_tensor *tensor) {

@@ -216,6 +216,13 @@ def lib():
                                                 _SZ, _P, _P, _P, _P, _P, _U32,
                                                 _U32, _U32, _U32, _U32, _F,
                                                 _U32, _U32, _U32, _F]),
+        "h3hip_refiner_create": (_P, [_P, _U32, _U32, _U32, _U32, _U32,
+                                      C.c_char_p, _SZ]),
+        "h3hip_refiner_free": (None, [_P]),
+        "h3hip_refiner_error": (C.c_char_p, [_P]),
+        "h3hip_refiner_tensor": (_P, [_P, C.c_char_p, _U32]),
+        "h3hip_refiner_init_random": (_I, [_P, C.c_uint64, _F]),
+        "h3hip_refiner_run": (_I, [_P, _P, _P, _U32]),
         "h3hip_dit_sampler_rows": (None, [_P, C.POINTER(_U32),
                                           C.POINTER(_U32), C.POINTER(_U32),
                                           C.POINTER(_U32)]),
@@ -553,6 +560,46 @@ def dit_config(family, hidden, heads, ffn, rows, blocks=1, text_rows=0,
 def block_flops(cfg):
     """FLOPs of one block (host math only, no device needed)."""
     return lib().h3hip_dit_block_flops(C.byref(cfg))
+
+
+class Refiner:
+    """The text token refiner (h3hip_refiner_*)."""
+
+    def __init__(self, gpu, hidden, heads, ffn, text_dim, head_dim=128):
+        self.gpu = gpu
+        err = C.create_string_buffer(512)
+        self.h = gpu.L.h3hip_refiner_create(gpu.h, hidden, heads, head_dim,
+                                            ffn, text_dim, err, 512)
+        if not self.h:
+            raise RuntimeError("h3hip_refiner_create failed: " +
+                               err.value.decode())
+
+    def close(self):
+        if self.h:
+            self.gpu.L.h3hip_refiner_free(self.h)
+            self.h = None
+
+    def _check(self, ok, what):
+        if not ok:
+            raise RuntimeError(what + ": " +
+                               self.gpu.L.h3hip_refiner_error(self.h).decode())
+
+    def tensor(self, name, block=0):
+        t = self.gpu.L.h3hip_refiner_tensor(self.h, name.encode(), block)
+        if not t:
+            raise KeyError(name)
+        return t
+
+    def read(self, name, block=0):
+        return self.gpu.read_bf16(self.tensor(name, block))
+
+    def init_random(self, seed, weight_std=0.02):
+        self._check(self.gpu.L.h3hip_refiner_init_random(self.h, seed,
+                                                         weight_std), "init")
+
+    def run(self, output, source, rows):
+        self._check(self.gpu.L.h3hip_refiner_run(self.h, output, source,
+                                                 rows), "refiner run")
 
 
 def safetensors_index(path):

@@ -1168,3 +1168,205 @@ long h3hip_dit_set_sparse_window(h3hip_dit *dit, const h3hip_layout *layout,
     }
     return total;
 }
+
+/* ----------------------------------------------------- text refiner */
+
+struct h3hip_refiner {
+    h3_gpu *gpu;
+    uint32_t hidden, heads, head_dim, ffn, text_dim;
+    h3_gpu_tensor *condition_w, *condition_b, *final_norm;
+    struct {
+        h3_gpu_tensor *norm1, *qkv, *q_norm, *k_norm, *out, *norm2, *fc1,
+            *fc2;
+    } block[2];
+    char error[512];
+};
+
+static int refiner_fail(h3hip_refiner *r, const char *what) {
+    snprintf(r->error, sizeof(r->error), "%s: %s", what,
+             h3_gpu_error(r->gpu));
+    return 0;
+}
+
+h3hip_refiner *h3hip_refiner_create(h3_gpu *gpu, uint32_t hidden,
+                                    uint32_t heads, uint32_t head_dim,
+                                    uint32_t ffn, uint32_t text_dim,
+                                    char *error, size_t error_size) {
+    if (!gpu || !hidden || !heads || !head_dim || !ffn || !text_dim) {
+        if (error && error_size)
+            snprintf(error, error_size, "invalid refiner configuration");
+        return NULL;
+    }
+    h3hip_refiner *r = (h3hip_refiner *)calloc(1, sizeof(*r));
+    if (!r) return NULL;
+    r->gpu = gpu;
+    r->hidden = hidden;
+    r->heads = heads;
+    r->head_dim = head_dim;
+    r->ffn = ffn;
+    r->text_dim = text_dim;
+    const size_t d = hidden, inner = (size_t)heads * head_dim, f = ffn;
+    int ok = 1;
+#define NEW(n) (ok && (t = h3_gpu_tensor_new_bf16(gpu, (n))) ? t : (ok = 0, NULL))
+    h3_gpu_tensor *t = NULL;
+    r->condition_w = NEW(d * text_dim);
+    r->condition_b = NEW(d);
+    r->final_norm = NEW(d);
+    for (int b = 0; b < 2; b++) {
+        r->block[b].norm1 = NEW(d);
+        r->block[b].qkv = NEW(3 * inner * d);
+        r->block[b].q_norm = NEW(head_dim);
+        r->block[b].k_norm = NEW(head_dim);
+        r->block[b].out = NEW(d * inner);
+        r->block[b].norm2 = NEW(d);
+        r->block[b].fc1 = NEW(2 * f * d);
+        r->block[b].fc2 = NEW(d * f);
+    }
+#undef NEW
+    if (!ok) {
+        if (error && error_size)
+            snprintf(error, error_size, "cannot allocate refiner weights: %s",
+                     h3_gpu_error(gpu));
+        h3hip_refiner_free(r);
+        return NULL;
+    }
+    return r;
+}
+
+void h3hip_refiner_free(h3hip_refiner *r) {
+    if (!r) return;
+    h3_gpu_tensor_free(r->condition_w);
+    h3_gpu_tensor_free(r->condition_b);
+    h3_gpu_tensor_free(r->final_norm);
+    for (int b = 0; b < 2; b++) {
+        h3_gpu_tensor **fields = (h3_gpu_tensor **)&r->block[b];
+        for (size_t i = 0; i < sizeof(r->block[b]) / sizeof(*fields); i++)
+            h3_gpu_tensor_free(fields[i]);
+    }
+    free(r);
+}
+
+const char *h3hip_refiner_error(const h3hip_refiner *r) {
+    return r ? r->error : "no refiner";
+}
+
+h3_gpu_tensor *h3hip_refiner_tensor(h3hip_refiner *r, const char *name,
+                                    uint32_t block) {
+    if (!r || !name) return NULL;
+    if (!strcmp(name, "condition_w")) return r->condition_w;
+    if (!strcmp(name, "condition_b")) return r->condition_b;
+    if (!strcmp(name, "final_norm")) return r->final_norm;
+    if (block > 1) return NULL;
+    struct { const char *name; h3_gpu_tensor *tensor; } table[] = {
+        {"norm1", r->block[block].norm1}, {"qkv", r->block[block].qkv},
+        {"q_norm", r->block[block].q_norm},
+        {"k_norm", r->block[block].k_norm}, {"out", r->block[block].out},
+        {"norm2", r->block[block].norm2}, {"fc1", r->block[block].fc1},
+        {"fc2", r->block[block].fc2}};
+    for (size_t i = 0; i < sizeof(table) / sizeof(*table); i++)
+        if (!strcmp(name, table[i].name)) return table[i].tensor;
+    return NULL;
+}
+
+static int refiner_fill(h3hip_refiner *r, h3_gpu_tensor *t, uint64_t *seed,
+                        float mean, float std) {
+    return h3_gpu_fill_normal_bf16(r->gpu, t, 0, h3_gpu_tensor_elements(t),
+                                   (*seed)++, mean, std);
+}
+
+int h3hip_refiner_init_random(h3hip_refiner *r, uint64_t seed,
+                              float weight_std) {
+    if (!r) return 0;
+    if (!h3_gpu_begin(r->gpu)) return refiner_fail(r, "begin refiner init");
+    uint64_t s = seed * 1000003ull + 29;
+    int ok = refiner_fill(r, r->condition_w, &s, 0.0f, weight_std) &&
+             refiner_fill(r, r->condition_b, &s, 0.0f, 0.02f) &&
+             refiner_fill(r, r->final_norm, &s, 1.0f, 0.02f);
+    for (int b = 0; b < 2 && ok; b++)
+        ok = refiner_fill(r, r->block[b].norm1, &s, 1.0f, 0.02f) &&
+             refiner_fill(r, r->block[b].qkv, &s, 0.0f, weight_std) &&
+             refiner_fill(r, r->block[b].q_norm, &s, 1.0f, 0.02f) &&
+             refiner_fill(r, r->block[b].k_norm, &s, 1.0f, 0.02f) &&
+             refiner_fill(r, r->block[b].out, &s, 0.0f, weight_std) &&
+             refiner_fill(r, r->block[b].norm2, &s, 1.0f, 0.02f) &&
+             refiner_fill(r, r->block[b].fc1, &s, 0.0f, weight_std) &&
+             refiner_fill(r, r->block[b].fc2, &s, 0.0f, weight_std);
+    if (!ok) {
+        refiner_fail(r, "refiner init");
+        (void)h3_gpu_submit(r->gpu);
+        return 0;
+    }
+    return h3_gpu_submit(r->gpu) ? 1 : refiner_fail(r, "refiner init");
+}
+
+int h3hip_refiner_run(h3hip_refiner *r, h3_gpu_tensor *output,
+                      const h3_gpu_tensor *source, uint32_t rows) {
+    if (!r) return 0;
+    h3_gpu *gpu = r->gpu;
+    const uint32_t d = r->hidden, hd = r->head_dim, heads = r->heads;
+    const uint32_t inner = heads * hd, f = r->ffn;
+    if (!rows || !output || !source ||
+        h3_gpu_tensor_elements(output) < (size_t)rows * d ||
+        h3_gpu_tensor_elements(source) < (size_t)rows * r->text_dim) {
+        snprintf(r->error, sizeof(r->error), "invalid refiner run");
+        return 0;
+    }
+    h3_gpu_tensor *norm = h3_gpu_tensor_new_bf16(gpu, (size_t)rows * d);
+    h3_gpu_tensor *qkv = h3_gpu_tensor_new_bf16(gpu, (size_t)rows * inner * 3);
+    h3_gpu_tensor *query = h3_gpu_tensor_new_bf16(gpu, (size_t)rows * inner);
+    h3_gpu_tensor *key = h3_gpu_tensor_new_bf16(gpu, (size_t)rows * inner);
+    h3_gpu_tensor *value = h3_gpu_tensor_new_bf16(gpu, (size_t)rows * inner);
+    h3_gpu_tensor *heads_out = h3_gpu_tensor_new_bf16(gpu,
+                                                      (size_t)rows * inner);
+    h3_gpu_tensor *branch = h3_gpu_tensor_new_bf16(gpu, (size_t)rows * d);
+    h3_gpu_tensor *fc1 = h3_gpu_tensor_new_bf16(gpu, (size_t)rows * f * 2);
+    h3_gpu_tensor *act = h3_gpu_tensor_new_bf16(gpu, (size_t)rows * f);
+    h3_gpu_tensor *scratch[] = {norm, qkv, query, key, value, heads_out,
+                                branch, fc1, act};
+    int ok = 1;
+    for (size_t i = 0; i < sizeof(scratch) / sizeof(*scratch); i++)
+        if (!scratch[i]) ok = 0;
+    if (!ok) refiner_fail(r, "cannot allocate refiner scratch");
+    const float scale = 1.0f / sqrtf((float)hd);
+    h3_gpu_tensor *x = output;
+#define STEP(call, what) (ok = ok && ((call) || refiner_fail(r, what)))
+    STEP(h3_gpu_begin(gpu), "begin token refinement");
+    int begun = ok;
+    STEP(h3_gpu_linear_bf16(gpu, x, source, r->condition_w, r->condition_b,
+                            rows, r->text_dim, d), "condition projection");
+    for (int b = 0; b < 2; b++) {
+        STEP(h3_gpu_rms_norm_bf16(gpu, norm, x, r->block[b].norm1, rows, d,
+                                  1e-5f), "refiner attention norm");
+        STEP(h3_gpu_linear_bf16(gpu, qkv, norm, r->block[b].qkv, NULL, rows,
+                                d, inner * 3), "refiner QKV");
+        /* rope_half 0: per-head RMS of q and k only, the tables unread */
+        STEP(h3_gpu_grouped_qkv_rope_bf16(gpu, query, key, value, qkv,
+                                          r->block[b].q_norm,
+                                          r->block[b].k_norm,
+                                          r->block[b].q_norm,
+                                          r->block[b].q_norm, rows, heads,
+                                          hd, 0, 1e-5f), "refiner QK norm");
+        STEP(h3_gpu_sdpa_bf16(gpu, heads_out, query, key, value, rows, heads,
+                              hd, scale), "refiner attention");
+        STEP(h3_gpu_linear_bf16(gpu, branch, heads_out, r->block[b].out, NULL,
+                                rows, inner, d), "refiner attention output");
+        STEP(h3_gpu_add_bf16(gpu, x, x, branch, (size_t)rows * d),
+             "refiner attention residual");
+        STEP(h3_gpu_rms_norm_bf16(gpu, norm, x, r->block[b].norm2, rows, d,
+                                  1e-5f), "refiner MLP norm");
+        STEP(h3_gpu_linear_bf16(gpu, fc1, norm, r->block[b].fc1, NULL, rows,
+                                d, f * 2), "refiner MLP input");
+        STEP(h3_gpu_swiglu_bf16(gpu, act, fc1, rows, f), "refiner SwiGLU");
+        STEP(h3_gpu_linear_bf16(gpu, branch, act, r->block[b].fc2, NULL, rows,
+                                f, d), "refiner MLP output");
+        STEP(h3_gpu_add_bf16(gpu, x, x, branch, (size_t)rows * d),
+             "refiner MLP residual");
+    }
+    STEP(h3_gpu_rms_norm_bf16(gpu, x, x, r->final_norm, rows, d, 1e-5f),
+         "refiner final norm");
+#undef STEP
+    if (begun && !h3_gpu_submit(gpu) && ok) ok = refiner_fail(r, "submit");
+    for (size_t i = 0; i < sizeof(scratch) / sizeof(*scratch); i++)
+        h3_gpu_tensor_free(scratch[i]);
+    return ok;
+}

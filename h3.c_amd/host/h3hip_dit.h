@@ -195,6 +195,34 @@ void h3hip_dit_sampler_rows(const h3hip_dit *dit, uint32_t *video_rows,
 
 const char *h3hip_dit_error(const h3hip_dit *dit);
 
+/* Text token refiner (reference refine_text / run_refiner_block,
+ * h3_dit.c:766-884): the text encoder's rows (text_dim wide) are projected
+ * to the model width with a biased linear, passed through two pre-norm
+ * self-attention + SwiGLU blocks with no RoPE and no modulation, and
+ * RMS-normalised.  Its weights are separate from the denoiser blocks; the
+ * shapes follow the DiT it refines for (hidden, heads x head_dim, ffn).
+ * Tensor names, block 0 or 1: "norm1" "qkv" "q_norm" "k_norm" "out" "norm2"
+ * "fc1" "fc2"; block ignored: "condition_w" [hidden x text_dim]
+ * "condition_b" [hidden] "final_norm" [hidden]. */
+typedef struct h3hip_refiner h3hip_refiner;
+
+h3hip_refiner *h3hip_refiner_create(h3_gpu *gpu, uint32_t hidden,
+                                    uint32_t heads, uint32_t head_dim,
+                                    uint32_t ffn, uint32_t text_dim,
+                                    char *error, size_t error_size);
+void h3hip_refiner_free(h3hip_refiner *refiner);
+const char *h3hip_refiner_error(const h3hip_refiner *refiner);
+h3_gpu_tensor *h3hip_refiner_tensor(h3hip_refiner *refiner,
+                                    const char *name, uint32_t block);
+/* Seeded device-side init: norms ~ N(1, 0.02^2), matrices
+ * ~ N(0, weight_std^2), the condition bias ~ N(0, 0.02^2). */
+int h3hip_refiner_init_random(h3hip_refiner *refiner, uint64_t seed,
+                              float weight_std);
+/* output [rows x hidden] BF16 <- refine(source [rows x text_dim] BF16).
+ * Runs in its own batch; scratch is allocated for the call and freed. */
+int h3hip_refiner_run(h3hip_refiner *refiner, h3_gpu_tensor *output,
+                      const h3_gpu_tensor *source, uint32_t rows);
+
 #ifdef __cplusplus
 }
 #endif

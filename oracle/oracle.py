@@ -361,6 +361,29 @@ def h3_blocks(hidden, blocks, row_map, cos, sin, rows, hidden_dim, heads, ffn,
     return x
 
 
+def refine_text(source, w, rows, text_dim, hidden_dim, heads, ffn, hd=128,
+                eps=1e-5):
+    """Text token refiner in the reference op order (refine_text and
+    run_refiner_block, h3_dit.c:766-884): biased condition projection, two
+    pre-norm blocks of RMSNorm -> QKV -> per-head q/k RMS (no RoPE) -> SDPA
+    -> out + residual, RMSNorm -> fc1 -> SwiGLU -> fc2 + residual, and a final
+    RMSNorm.  w: condition_w, condition_b, final_norm, blocks[2] of dicts
+    with norm1, qkv, q_norm, k_norm, out, norm2, fc1, fc2 (bf16 bits)."""
+    inner = heads * hd
+    x = linear(source, w["condition_w"], w["condition_b"], rows, text_dim,
+               hidden_dim)
+    for b in w["blocks"]:
+        n = rms_norm(x, b["norm1"], rows, hidden_dim, eps)
+        qkv = linear(n, b["qkv"], None, rows, hidden_dim, 3 * inner)
+        q, k, v = qkv_rope(qkv, b["q_norm"], b["k_norm"], b["q_norm"],
+                           b["q_norm"], rows, heads, hd, 0, True, eps)
+        o = sdpa(q, k, v, rows, rows, heads, hd, 1.0 / math.sqrt(hd))
+        x = add(x, linear(o, b["out"], None, rows, inner, hidden_dim))
+        n = rms_norm(x, b["norm2"], rows, hidden_dim, eps)
+        x = add(x, mlp(n, b["fc1"], b["fc2"], rows, hidden_dim, ffn))
+    return rms_norm(x, w["final_norm"], rows, hidden_dim, eps)
+
+
 def reuse_schedule(steps, interval):
     """Evaluated steps under velocity reuse (h3_dit.c:2672-2687)."""
     return [interval == 1 or s == 0 or s == steps - 1 or s % interval == 0
