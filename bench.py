@@ -376,6 +376,11 @@ def main():
     ap.add_argument("--blocks", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-h3", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="only the Wan 512x512 forward and its per-class "
+                         "replays (no attention sweep, 864x480 forward, H3 "
+                         "shape or weight loading): the run whose rocprof "
+                         "kernel averages match the line's own")
     ap.add_argument("--profile-pass", action="store_true",
                     help="for rocprofv3 runs: one forward, one replay of the "
                          "plain GEMMs, one 64 Mi-element copy-like kernel of "
@@ -431,18 +436,21 @@ def main():
     per_launch_ms = gemm_ms / (blocks * plain_launches)
     dit.close()
 
-    log("attention sweep and the 864x480 forward ...")
-    sweep = attention_sweep(gpu)
-    wan_big = wan_864x480(gpu, blocks, max(2, args.steps // 2))
+    sweep = wan_big = loading = None
+    if not args.no_extras:
+        log("attention sweep and the 864x480 forward ...")
+        sweep = attention_sweep(gpu)
+        wan_big = wan_864x480(gpu, blocks, max(2, args.steps // 2))
 
     h3_real = None
     denoise = None
-    if not args.no_h3:
+    if not args.no_h3 and not args.no_extras:
         log("H3 real shape: forward + 20-step Euler denoise ...")
         h3_real, denoise = h3_measure(gpu, blocks, max(2, args.steps // 2))
 
-    log("weight file loading ...")
-    loading = weight_load()
+    if not args.no_extras:
+        log("weight file loading ...")
+        loading = weight_load()
 
     base = None
     if not args.no_cpu_baseline:
