@@ -491,3 +491,108 @@ def test_token_pool_expand_pins():
     np.testing.assert_array_equal(z[0], f64(moved).reshape(3, width)[0])
     np.testing.assert_array_equal(z[2:], want[2:] * 0 +
                                   f64(orig).reshape(input_rows, width)[2:])
+
+
+# ------------------------------------------------------ sampler and refiner
+
+def test_reuse_schedule_and_ratio_literals():
+    """oracle.reuse_schedule against the reference's literals
+    (tests/test_h3.c:128-147) and the ratio's clamp (h3_dit.c:2644-2655)."""
+    sel = oracle.reuse_schedule(20, 3)
+    assert [s for s in range(20) if sel[s]] == [0, 3, 6, 9, 12, 15, 18, 19]
+    assert sum(oracle.reuse_schedule(20, 2)) == 11
+    assert sum(oracle.reuse_schedule(50, 3)) == 18
+    assert all(oracle.reuse_schedule(20, 1))
+    r = oracle.extrapolation_ratio
+    assert r(0.5, 0.6, 0.7, True) == pytest.approx(1.0)
+    assert r(0.5, 0.6, 0.7, False) == 0.0
+    assert r(0.5, 0.6, 0.6, True) == 0.0
+    assert r(0.0, 0.6, 0.65, True) == 2.0 and r(1.0, 0.6, 0.65, True) == -2.0
+
+
+def _denoise_with_velocity(monkeypatch, velocity, sigmas, reuse):
+    """oracle.h3_denoise with the forward replaced by velocity(sigma)."""
+    nv, na = 6, 4
+    m = dict(video_patch=2, audio_channels=2, video_conditions=1,
+             audio_conditions=0,
+             video_input=np.linspace(-1, 1, 2 * (nv // 2 + 1)).astype(
+                 np.float32),
+             audio_input=np.linspace(2, 3, na).astype(np.float32))
+
+    def forward(mm, step):
+        v = velocity(sigmas[step])
+        return b(np.full(nv, v)), b(np.full(na, -v))
+
+    monkeypatch.setattr(oracle, "h3_forward_step", forward)
+    return m, oracle.h3_denoise(m, sigmas, sigmas, reuse)
+
+
+def test_denoise_loop_constant_velocity(monkeypatch):
+    """Constant v: every step, fresh or extrapolated, moves x by
+    (sigma_i - sigma_i+1) v, so x_N = x_0 + (sigma_0 - sigma_N) v; the
+    condition rows ahead of the targets are untouched."""
+    sig = np.linspace(1.0, 0.0, 11).astype(np.float32)
+    for reuse in (1, 2, 3):
+        m, (video, audio, n) = _denoise_with_velocity(
+            monkeypatch, lambda s: 0.75, sig, reuse)
+        assert n == sum(oracle.reuse_schedule(10, reuse))
+        v0, a0 = m["video_input"], m["audio_input"]
+        assert np.array_equal(video[:2], v0[:2])
+        np.testing.assert_allclose(video[2:], v0[2:] + 0.75, atol=2e-6)
+        np.testing.assert_allclose(audio, a0 - 0.75, atol=2e-6)
+
+
+def test_denoise_extrapolation_is_exact_for_linear_velocity(monkeypatch):
+    """v(sigma) = sigma: the reuse extrapolation v_last + r (v_last - v_prev)
+    with r = (s - s_last) / (s_last - s_prev) reproduces v(s) on skipped
+    steps, except the first skipped step, which has no previous evaluation
+    and holds v(s_0) (ratio 0).  So reuse 2 lands where evaluating every
+    step does plus that one step's (s_1 - s_2)(s_0 - s_1), to bf16 rounding
+    of the velocities, and every-step evaluation follows
+    sum (s_i - s_i+1) s_i.  A wrong sign of r, a stale v_prev or the wrong
+    sigma pair fails this."""
+    sig = np.linspace(1.0, 0.0, 9).astype(np.float32)
+    _, (v_all, _, n1) = _denoise_with_velocity(monkeypatch, lambda s: s, sig,
+                                                1)
+    _, (v_re, _, n2) = _denoise_with_velocity(monkeypatch, lambda s: s, sig,
+                                               2)
+    assert (n1, n2) == (8, 5)
+    exact = sum((sig[i] - sig[i + 1]) * sig[i] for i in range(8))
+    x0 = np.linspace(-1, 1, 8).astype(np.float32)[2:]
+    np.testing.assert_allclose(v_all[2:], x0 + exact, atol=4e-3)
+    first_hold = (sig[1] - sig[2]) * (sig[0] - sig[1])
+    np.testing.assert_allclose(v_re[2:], v_all[2:] + first_hold, atol=4e-3)
+    # no reuse at all would drift: constant-hold of the last velocity
+    held = sum((sig[i] - sig[i + 1]) * sig[i - (i % 2)] for i in range(8))
+    assert abs(held - exact) > 0.02
+
+
+def test_refiner_with_zero_branches_is_norm_of_projection():
+    """Zero out-projection and fc2 weights make both residual branches add
+    exact zeros, so refine_text reduces to the final RMSNorm of the biased
+    condition projection (h3_dit.c:851-866), bit for bit; nonzero branches
+    must change it."""
+    rows, td, d, heads, ffn = 5, 64, 256, 2, 128
+    r = np.random.default_rng(9)
+    w = {"condition_w": b(r.standard_normal(d * td) * 0.1),
+         "condition_b": b(r.standard_normal(d) * 0.1),
+         "final_norm": b(1 + 0.05 * r.standard_normal(d))}
+    blocks = []
+    for _ in range(2):
+        blocks.append({
+            "norm1": b(1 + 0.05 * r.standard_normal(d)),
+            "qkv": b(r.standard_normal(3 * 256 * d) * 0.05),
+            "q_norm": b(np.ones(128)), "k_norm": b(np.ones(128)),
+            "out": b(np.zeros(d * 256)),
+            "norm2": b(1 + 0.05 * r.standard_normal(d)),
+            "fc1": b(r.standard_normal(2 * ffn * d) * 0.05),
+            "fc2": b(np.zeros(d * ffn))})
+    w["blocks"] = blocks
+    src = b(r.standard_normal(rows * td))
+    got = oracle.refine_text(src, w, rows, td, d, heads, ffn)
+    proj = oracle.linear(src, w["condition_w"], w["condition_b"], rows, td, d)
+    assert np.array_equal(got, oracle.rms_norm(proj, w["final_norm"], rows,
+                                               d, 1e-5))
+    blocks[1]["fc2"] = b(r.standard_normal(d * ffn) * 0.05)
+    assert not np.array_equal(
+        oracle.refine_text(src, w, rows, td, d, heads, ffn), got)

@@ -68,7 +68,8 @@ def test_sparse_mask_structure_on_the_real_layout():
 
 def test_oracle_sparse_sdpa_pins():
     """Full lists reproduce the dense oracle bit for bit; a block with one
-    listed tile equals dense attention over that tile's keys alone."""
+    listed tile equals dense attention over that tile's keys alone; an
+    empty list gives zeros."""
     rng = np.random.default_rng(4)
     n, h, hd = 200, 2, 128
     q, k, v = (oracle.bf16(rng.standard_normal(n * h * hd).astype(np.float32))
@@ -85,3 +86,8 @@ def test_oracle_sparse_sdpa_pins():
                        hd, scale)
     got = one.reshape(n, h, hd)[:128].ravel()
     assert np.array_equal(got, want)
+    # a block whose list is empty outputs zeros (the reference's l = 0
+    # guard, h3_cuda_attention.cu:1789)
+    empty = oracle.sdpa_sparse(q, k, v, n, h, hd, scale, [0, 0, 1], [3])
+    assert not empty.reshape(n, h, hd)[:128].any()
+    assert empty.reshape(n, h, hd)[128:].any()
