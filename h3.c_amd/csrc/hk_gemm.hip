@@ -96,6 +96,11 @@ struct hk_gemm_args {
     uint32_t m, n, k;      /* n = output columns */
     uint32_t tiles_m, tiles_n;
     uint32_t x_bytes, w_bytes;
+    /* split-K (EPI == HK_EPI_PARTIAL only): workgroup pid covers tile
+     * pid % tiles of K steps [split * split_steps, +split_steps), and
+     * writes F32 partial[split][M][N] */
+    float *partial;
+    uint32_t split_steps;
 };
 
 template <int EPI>
@@ -111,6 +116,13 @@ hk_gemm_mfma(hk_gemm_args g) {
     uint32_t pid = blockIdx.x;
     const uint32_t nwg = gridDim.x;
     if ((nwg & 7u) == 0) pid = (pid & 7u) * (nwg >> 3) + (pid >> 3);
+    uint32_t k_first = 0, split = 0;
+    if (EPI == HK_EPI_PARTIAL) {
+        const uint32_t tiles = g.tiles_m * g.tiles_n;
+        split = pid / tiles;
+        pid -= split * tiles;
+        k_first = split * g.split_steps;
+    }
     const uint32_t band = HK_GROUP_M * g.tiles_n;
     const uint32_t first_m = (pid / band) * HK_GROUP_M;
     const uint32_t band_rows = min(g.tiles_m - first_m, (uint32_t)HK_GROUP_M);
@@ -136,7 +148,7 @@ hk_gemm_mfma(hk_gemm_args g) {
         const uint32_t row = slot >> 3;
         const uint32_t chunk = (slot & 7u) ^ hk_swz_key(row);
         const uint32_t xm = min(m0 + row, g.m);
-        x_off[j] = xm * g.k * 2u + chunk * 16u;
+        x_off[j] = xm * g.k * 2u + chunk * 16u + k_first * (HK_BK * 2u);
         uint32_t wrow;
         if (EPI == HK_EPI_SWIGLU) {
             /* W tile rows: per wave half 64 gate rows then 64 up rows */
@@ -146,7 +158,7 @@ hk_gemm_mfma(hk_gemm_args g) {
         } else {
             wrow = min(tile_n * HK_BN + row, g.n);
         }
-        w_off[j] = wrow * g.k * 2u + chunk * 16u;
+        w_off[j] = wrow * g.k * 2u + chunk * 16u + k_first * (HK_BK * 2u);
     }
 
     hk_f32x16 acc[4][4];
@@ -190,7 +202,9 @@ hk_gemm_mfma(hk_gemm_args g) {
      * there, one after each of those 16 MFMAs: the load issue hides under
      * the matrix pipe, and every load has a full stage (64 MFMAs per wave)
      * plus a phase to land before the barrier that waits for it. */
-    const uint32_t k_steps = g.k / HK_BK;
+    const uint32_t k_steps =
+        EPI == HK_EPI_PARTIAL ? min(g.split_steps, g.k / HK_BK - k_first)
+                              : g.k / HK_BK;
     const uint32_t frag_row = lane & 31u;
     const uint32_t frag_half = lane >> 5;
     const uint32_t lds_base =
@@ -300,7 +314,20 @@ hk_gemm_mfma(hk_gemm_args g) {
         const uint32_t m = m0 + wm * 128u + j * 32u + frag_row;
         if (m >= g.m) continue;
         uint16_t *crow = g.c + (size_t)m * g.n;
-        if (EPI == HK_EPI_SWIGLU) {
+        if (EPI == HK_EPI_PARTIAL) {
+            float *prow = g.partial + ((size_t)split * g.m + m) * g.n;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const uint32_t col = tile_n * HK_BN + wn * 128u + i * 32u +
+                                         q * 8u + sub;
+                    if (col >= g.n) continue;
+                    *(float4 *)(prow + col) =
+                        make_float4(acc[i][j][q * 4], acc[i][j][q * 4 + 1],
+                                    acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]);
+                }
+        } else if (EPI == HK_EPI_SWIGLU) {
 #pragma unroll
             for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -456,6 +483,33 @@ __global__ void hk_swiglu_rows(const uint16_t *fused, uint16_t *out,
 
 static bool hk_gemm_lds_ready = false;
 
+/* Split-K reduction: C = bf16(sum_s partial[s] + bias), four columns per
+ * thread (N % 4 == 0). */
+__global__ void hk_splitk_reduce(const float *__restrict__ partial,
+                                 const uint16_t *__restrict__ bias,
+                                 uint16_t *__restrict__ c, uint32_t m,
+                                 uint32_t n, uint32_t splits) {
+    const size_t quad = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t count = (size_t)m * n;
+    if (quad * 4 >= count) return;
+    const size_t e = quad * 4;
+    float4 sum = *(const float4 *)(partial + e);
+    for (uint32_t s = 1; s < splits; s++) {
+        const float4 p = *(const float4 *)(partial + s * count + e);
+        sum.x += p.x; sum.y += p.y; sum.z += p.z; sum.w += p.w;
+    }
+    if (bias) {
+        const uint32_t col = (uint32_t)(e % n);
+        const uint2 b = *(const uint2 *)(bias + col);
+        sum.x += hk_bf2f(b.x & 0xffffu);
+        sum.y += hk_bf2f(b.x >> 16);
+        sum.z += hk_bf2f(b.y & 0xffffu);
+        sum.w += hk_bf2f(b.y >> 16);
+    }
+    *(uint2 *)(c + e) = make_uint2(hk_pack2(sum.x, sum.y),
+                                   hk_pack2(sum.z, sum.w));
+}
+
 int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
                  const uint16_t *bias, uint16_t *c, uint32_t m, uint32_t n,
                  uint32_t k, int epilogue) {
@@ -485,6 +539,9 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
             (void)hipFuncSetAttribute(
                 (const void *)hk_gemm_mfma<HK_EPI_GELU>,
                 hipFuncAttributeMaxDynamicSharedMemorySize, HK_GEMM_LDS);
+            (void)hipFuncSetAttribute(
+                (const void *)hk_gemm_mfma<HK_EPI_PARTIAL>,
+                hipFuncAttributeMaxDynamicSharedMemorySize, HK_GEMM_LDS);
             hk_gemm_lds_ready = true;
         }
         hk_gemm_args g;
@@ -495,7 +552,35 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
         g.tiles_n = (n + cols_per_tile - 1) / cols_per_tile;
         g.x_bytes = (uint32_t)x_bytes;
         g.w_bytes = (uint32_t)w_bytes;
+        g.partial = NULL;
+        g.split_steps = 0;
         dim3 grid(g.tiles_m * g.tiles_n);
+        /* Split-K when the tiles would leave over half the CUs idle (the
+         * 512-row cross-attention K/V projections: 40 tiles): each of up to
+         * num_cus / tiles workgroups per tile takes at least 8 K steps, and
+         * a reduction adds the F32 partials, the bias and rounds. */
+        const uint32_t tiles = g.tiles_m * g.tiles_n;
+        const uint32_t k_steps = k / HK_BK;
+        const uint32_t cus = gpu->num_cus > 0 ? (uint32_t)gpu->num_cus : 256u;
+        if (epilogue == HK_EPI_STORE && tiles * 2 <= cus && k_steps >= 16) {
+            uint32_t splits = min(cus / tiles, k_steps / 8);
+            const uint32_t steps = (k_steps + splits - 1) / splits;
+            splits = (k_steps + steps - 1) / steps;
+            const size_t count = (size_t)m * n;
+            float *partial =
+                (float *)hk_splitk_space(gpu, (size_t)splits * count * 4);
+            if (!partial) return 0;
+            g.partial = partial;
+            g.split_steps = steps;
+            hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_PARTIAL>,
+                               dim3(tiles * splits), dim3(HK_GEMM_THREADS),
+                               HK_GEMM_LDS, gpu->stream, g);
+            hipLaunchKernelGGL(hk_splitk_reduce,
+                               dim3((unsigned)((count / 4 + 255) / 256)),
+                               dim3(256), 0, gpu->stream, partial, bias, c, m,
+                               n, splits);
+            return 1;
+        }
         if (epilogue == HK_EPI_SWIGLU)
             hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_SWIGLU>, grid,
                                dim3(HK_GEMM_THREADS), HK_GEMM_LDS, gpu->stream,

@@ -47,6 +47,8 @@ struct h3_gpu {
     /* grow-only device scratch for op intermediates */
     void *workspace;
     size_t workspace_bytes;
+    void *splitk; /* f32 partial tiles of split-K GEMMs */
+    size_t splitk_bytes;
     /* H3_HIP_REFERENCE=1: route GEMM and attention through the simple
      * (sequential-k / two-pass) reference kernels */
     int reference_kernels;
@@ -115,6 +117,9 @@ int hk_op_end(struct h3_gpu *gpu, const char *name, int kind);
 
 /* Grow-only device scratch shared by ops of one context. */
 void *hk_workspace(struct h3_gpu *gpu, size_t bytes);
+/* Grow-only scratch for split-K partials, separate from the workspace
+ * (which may hold a GEMM's input, e.g. the MLP activation). */
+void *hk_splitk_space(struct h3_gpu *gpu, size_t bytes);
 
 double hk_now(void);
 
@@ -124,7 +129,8 @@ double hk_now(void);
  */
 
 /* GEMM epilogues */
-enum { HK_EPI_STORE = 0, HK_EPI_SWIGLU = 1, HK_EPI_GELU = 2 };
+enum { HK_EPI_STORE = 0, HK_EPI_SWIGLU = 1, HK_EPI_GELU = 2,
+       HK_EPI_PARTIAL = 3 /* internal: f32 split-K partial tiles */ };
 
 /* C[M,N] = epi(A[M,K] . W[N,K]^T + bias).  For HK_EPI_SWIGLU the weight has
  * 2*N rows (gate rows [0,N), up rows [N,2N)) and C is the [M,N] activation.

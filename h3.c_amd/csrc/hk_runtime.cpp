@@ -110,27 +110,37 @@ static void hk_device_release(struct h3_gpu *gpu, void *data, size_t bytes) {
     }
 }
 
-void *hk_workspace(struct h3_gpu *gpu, size_t bytes) {
+static void *hk_grow(struct h3_gpu *gpu, void **buffer, size_t *have,
+                     size_t bytes, const char *what) {
     if (!bytes) bytes = 1;
-    if (gpu->workspace && bytes <= gpu->workspace_bytes)
-        return gpu->workspace;
-    size_t capacity = gpu->workspace_bytes ? gpu->workspace_bytes : 1u << 20;
+    if (*buffer && bytes <= *have) return *buffer;
+    size_t capacity = *have ? *have : 1u << 20;
     while (capacity < bytes) capacity *= 2;
     /* in-flight kernels may still read the old block */
     (void)hipStreamSynchronize(gpu->stream);
-    if (gpu->workspace) (void)hipFree(gpu->workspace);
-    gpu->workspace = NULL;
-    gpu->workspace_bytes = 0;
+    if (*buffer) (void)hipFree(*buffer);
+    *buffer = NULL;
+    *have = 0;
     void *fresh = NULL;
     hipError_t status = hipMalloc(&fresh, capacity);
     if (status != hipSuccess) {
         (void)hipGetLastError();
-        hk_fail_hip(gpu, "workspace allocation", status);
+        hk_fail_hip(gpu, what, status);
         return NULL;
     }
-    gpu->workspace = fresh;
-    gpu->workspace_bytes = capacity;
+    *buffer = fresh;
+    *have = capacity;
     return fresh;
+}
+
+void *hk_workspace(struct h3_gpu *gpu, size_t bytes) {
+    return hk_grow(gpu, &gpu->workspace, &gpu->workspace_bytes, bytes,
+                   "workspace allocation");
+}
+
+void *hk_splitk_space(struct h3_gpu *gpu, size_t bytes) {
+    return hk_grow(gpu, &gpu->splitk, &gpu->splitk_bytes, bytes,
+                   "split-K scratch allocation");
 }
 
 /* --------------------------------------------------------------- timing */
@@ -384,6 +394,7 @@ extern "C" void h3_gpu_free(h3_gpu *gpu) {
                 gpu->stats.command_wait_seconds);
     hk_cache_evict(gpu, 0);
     if (gpu->workspace) (void)hipFree(gpu->workspace);
+    if (gpu->splitk) (void)hipFree(gpu->splitk);
     if (gpu->sparse_ptr) (void)hipFree(gpu->sparse_ptr);
     if (gpu->sparse_idx) (void)hipFree(gpu->sparse_idx);
     hk_loader_free(gpu);

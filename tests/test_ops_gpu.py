@@ -33,12 +33,15 @@ def _mod_setup(rng, rows, width, slots=6, mod_rows=4):
     (32, 256, 256, False),      # reference test_cuda_core.c linear shape
     (100, 512, 768, True),      # ragged M
     (1, 256, 512, False),       # single row
-    (300, 5376, 1024, False),   # real K (hidden)
-    (257, 1024, 1280, True),    # M just past a tile
+    (300, 5376, 1024, False),   # real K (hidden); split-K (8 tiles)
+    (257, 1024, 1280, True),    # M just past a tile; split-K in 2
     (64, 96, 256, True),        # K % 64 != 0 -> sequential fallback kernel
     (39, 2688, 4100, True),     # skinny path: time rows x modulation width
     (64, 128, 68, False),       # skinny path: full 64-row tile, ragged N
     (65, 192, 256, False),      # one row past the skinny limit
+    (512, 5120, 5120, True),    # split-K: Wan cross K/V projection (40 tiles)
+    (260, 2048, 516, True),     # split-K, ragged M and N, 4 splits
+    (600, 1088, 256, False),    # split-K with a short last split (17 steps)
 ])
 def test_linear_bf16(gpu, m, k, n, bias):
     rng = np.random.default_rng(m * 7 + k + n)
