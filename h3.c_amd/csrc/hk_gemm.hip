@@ -198,10 +198,11 @@ hk_gemm_mfma(hk_gemm_args g) {
      * wait phases so the scheduler cannot fold them back together.  The
      * stage barrier sits before the last 16 MFMAs of a stage: by then every
      * wave holds all of the stage's fragments in registers, so the stage's
-     * LDS is free.  The loads of the stage after next go into it right
-     * there, one after each of those 16 MFMAs: the load issue hides under
-     * the matrix pipe, and every load has a full stage (64 MFMAs per wave)
-     * plus a phase to land before the barrier that waits for it. */
+     * LDS is free.  The loads of the stage after next go into it from there:
+     * the first half one per two of those 16 MFMAs, the second half one per
+     * two MFMAs of the next stage's first substep (a burst of 16 loads per
+     * wave stalls issue).  Every load still has over two substeps to land
+     * before the barrier that waits for it. */
     const uint32_t k_steps =
         EPI == HK_EPI_PARTIAL ? min(g.split_steps, g.k / HK_BK - k_first)
                               : g.k / HK_BK;
@@ -261,7 +262,7 @@ hk_gemm_mfma(hk_gemm_args g) {
      * in the last substep of a stage, the 16 loads of the stage after next
      * one per MFMA. */
     auto substep = [&](int buf, uint32_t rstage, int rks, bool loading,
-                       uint32_t lstage, uint32_t kb) {
+                       uint32_t lstage, uint32_t kb, int load_base) {
 #pragma unroll
         for (int t = 0; t < 16; t++) {
             const int i = t >> 2, j = t & 3;
@@ -270,7 +271,8 @@ hk_gemm_mfma(hk_gemm_args g) {
                 __builtin_bit_cast(hk_bf16x8, fx[buf][j]), acc[i][j], 0, 0,
                 0);
             if (t & 1) read_one(buf ^ 1, rstage, rks, t >> 1);
-            if (loading) issue_load(lstage, kb, t);
+            if (loading && (t & 1))
+                issue_load(lstage, kb, load_base + (t >> 1));
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -284,11 +286,14 @@ hk_gemm_mfma(hk_gemm_args g) {
 #define HK_PIN() __builtin_amdgcn_sched_barrier(0)
     for (uint32_t kt = 0; kt < k_steps; kt++) {
         const uint32_t stage = kt & 1u;
-        substep(0, stage, 1, false, 0, 0);
+        /* the second half of stage kt + 1's loads (the prologue issued all
+         * of stage 1's) */
+        substep(0, stage, 1, kt > 0, stage ^ 1u,
+                min(kt + 1, k_steps - 1) * HK_BK * 2u, 8);
         wait_frags(1);
-        substep(1, stage, 2, false, 0, 0);
+        substep(1, stage, 2, false, 0, 0, 0);
         wait_frags(0);
-        substep(0, stage, 3, false, 0, 0);
+        substep(0, stage, 3, false, 0, 0, 0);
         wait_frags(1);
         /* every wave now holds the whole stage in registers; the next stage
          * is complete once every wave's loads have landed */
@@ -299,7 +304,7 @@ hk_gemm_mfma(hk_gemm_args g) {
          * again, which keeps the loop free of branches around the
          * accumulators */
         substep(1, stage ^ 1u, 0, true, stage,
-                min(kt + 2, k_steps - 1) * HK_BK * 2u);
+                min(kt + 2, k_steps - 1) * HK_BK * 2u, 0);
         wait_frags(0);
     }
 #undef HK_PIN
@@ -307,14 +312,20 @@ hk_gemm_mfma(hk_gemm_args g) {
     /* ---- epilogue ----
      * acc[i][j][r] = C[m][n] with
      *   m = m0 + wm*128 + j*32 + lane%32
-     *   W-tile row = wn*128 + i*32 + (r/4)*8 + (lane/32)*4 + r%4 */
+     *   W-tile row = wn*128 + i*32 + (r/4)*8 + (lane/32)*4 + r%4
+     * Each lane holds 4 consecutive columns of 16 rows per (i, j), so direct
+     * stores would write 8 bytes into 32 different rows per instruction.
+     * Instead the finished bf16 tile goes through LDS (free once the last
+     * stage's loads have landed) and leaves as whole rows, 16 bytes per
+     * lane.  LDS rows are `pitch` bytes; 16-byte chunk c of row r sits at
+     * chunk c ^ (r % chunks), so both the 8-byte fragment writes (32 rows,
+     * one column group) and the row reads spread over the banks. */
     const uint32_t sub = frag_half * 4u;
+    if (EPI == HK_EPI_PARTIAL) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const uint32_t m = m0 + wm * 128u + j * 32u + frag_row;
-        if (m >= g.m) continue;
-        uint16_t *crow = g.c + (size_t)m * g.n;
-        if (EPI == HK_EPI_PARTIAL) {
+        for (int j = 0; j < 4; j++) {
+            const uint32_t m = m0 + wm * 128u + j * 32u + frag_row;
+            if (m >= g.m) continue;
             float *prow = g.partial + ((size_t)split * g.m + m) * g.n;
 #pragma unroll
             for (int i = 0; i < 4; i++)
@@ -327,14 +338,27 @@ hk_gemm_mfma(hk_gemm_args g) {
                         make_float4(acc[i][j][q * 4], acc[i][j][q * 4 + 1],
                                     acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]);
                 }
-        } else if (EPI == HK_EPI_SWIGLU) {
+        }
+        return;
+    }
+    constexpr uint32_t tile_cols = EPI == HK_EPI_SWIGLU ? 128u : HK_BN;
+    constexpr uint32_t pitch = tile_cols * 2u;     /* bytes per LDS row */
+    constexpr uint32_t chunks = pitch / 16u;
+    const uint32_t n0 = tile_n * tile_cols;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    auto lds_put = [&](uint32_t row, uint32_t col, uint2 v) {
+        const uint32_t chunk = (col >> 3) ^ (row & (chunks - 1u));
+        *(uint2 *)(hk_smem + row * pitch + chunk * 16u + (col & 7u) * 2u) = v;
+    };
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t row = wm * 128u + j * 32u + frag_row;
+        if (EPI == HK_EPI_SWIGLU) {
 #pragma unroll
             for (int i = 0; i < 2; i++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const uint32_t col = tile_n * 128u + wn * 64u + i * 32u +
-                                         q * 8u + sub;
-                    if (col >= g.n) continue;
                     float out[4];
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
@@ -342,23 +366,21 @@ hk_gemm_mfma(hk_gemm_args g) {
                         float up = hk_bf2f(hk_f2bf(acc[i + 2][j][q * 4 + e]));
                         out[e] = hk_silu_f(gate) * up;
                     }
-                    uint2 packed = {hk_pack2(out[0], out[1]),
-                                    hk_pack2(out[2], out[3])};
-                    *(uint2 *)(crow + col) = packed;
+                    lds_put(row, wn * 64u + i * 32u + q * 8u + sub,
+                            make_uint2(hk_pack2(out[0], out[1]),
+                                       hk_pack2(out[2], out[3])));
                 }
         } else {
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const uint32_t col = tile_n * HK_BN + wn * 128u + i * 32u +
-                                         q * 8u + sub;
-                    if (col >= g.n) continue;
+                    const uint32_t tcol = wn * 128u + i * 32u + q * 8u + sub;
                     float out[4];
 #pragma unroll
                     for (int e = 0; e < 4; e++) out[e] = acc[i][j][q * 4 + e];
-                    if (g.bias) {
-                        uint2 b = *(const uint2 *)(g.bias + col);
+                    if (g.bias && n0 + tcol < g.n) {
+                        uint2 b = *(const uint2 *)(g.bias + n0 + tcol);
                         out[0] += hk_bf2f(b.x & 0xffffu);
                         out[1] += hk_bf2f(b.x >> 16);
                         out[2] += hk_bf2f(b.y & 0xffffu);
@@ -369,11 +391,29 @@ hk_gemm_mfma(hk_gemm_args g) {
                         for (int e = 0; e < 4; e++)
                             out[e] = hk_gelu_tanh_f(hk_bf2f(hk_f2bf(out[e])));
                     }
-                    uint2 packed = {hk_pack2(out[0], out[1]),
-                                    hk_pack2(out[2], out[3])};
-                    *(uint2 *)(crow + col) = packed;
+                    lds_put(row, tcol,
+                            make_uint2(hk_pack2(out[0], out[1]),
+                                       hk_pack2(out[2], out[3])));
                 }
         }
+    }
+    __syncthreads();
+    /* rows leave 16 bytes per lane; N % 4 == 0, so a chunk is either whole,
+     * its first 8 bytes, or past the end */
+    constexpr uint32_t rows_per_pass = HK_GEMM_THREADS / chunks;
+    const uint32_t chunk = tid % chunks;
+    const uint32_t col = n0 + chunk * 8u;
+#pragma unroll 4
+    for (uint32_t row = tid / chunks; row < HK_BM; row += rows_per_pass) {
+        const uint32_t m = m0 + row;
+        if (m >= g.m || col >= g.n) continue;
+        const uint8_t *src = hk_smem + row * pitch +
+                             ((chunk ^ (row & (chunks - 1u))) << 4);
+        uint16_t *dst = g.c + (size_t)m * g.n + col;
+        if (col + 8u <= g.n)
+            *(uint4 *)dst = *(const uint4 *)src;
+        else
+            *(uint2 *)dst = *(const uint2 *)src;
     }
 }
 
