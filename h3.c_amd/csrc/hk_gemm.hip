@@ -97,11 +97,26 @@ struct hk_gemm_args {
     uint32_t tiles_m, tiles_n;
     uint32_t x_bytes, w_bytes;
     /* split-K (EPI == HK_EPI_PARTIAL only): workgroup pid covers tile
-     * pid % tiles of K steps [split * split_steps, +split_steps), and
-     * writes F32 partial[split][M][N] */
+     * tile_base + pid % part_tiles over K steps [split * split_steps,
+     * +split_steps), split = pid / part_tiles, and writes the F32 tile to
+     * partial[split][pid % part_tiles][256][256] */
     float *partial;
-    uint32_t split_steps;
+    uint32_t split_steps, tile_base, part_tiles;
 };
+
+/* Tile index -> (tile_m, tile_n): column bands of HK_GROUP_M row tiles, so
+ * consecutive tiles share W rows (and, band by band, X rows). */
+__device__ __forceinline__ void hk_tile_coords(uint32_t tile, uint32_t tiles_m,
+                                               uint32_t tiles_n,
+                                               uint32_t &tile_m,
+                                               uint32_t &tile_n) {
+    const uint32_t band = HK_GROUP_M * tiles_n;
+    const uint32_t first_m = (tile / band) * HK_GROUP_M;
+    const uint32_t band_rows = min(tiles_m - first_m, (uint32_t)HK_GROUP_M);
+    const uint32_t in_band = tile % band;
+    tile_m = first_m + in_band % band_rows;
+    tile_n = in_band / band_rows;
+}
 
 template <int EPI>
 __global__ void __launch_bounds__(HK_GEMM_THREADS, 1)
@@ -116,19 +131,15 @@ hk_gemm_mfma(hk_gemm_args g) {
     uint32_t pid = blockIdx.x;
     const uint32_t nwg = gridDim.x;
     if ((nwg & 7u) == 0) pid = (pid & 7u) * (nwg >> 3) + (pid >> 3);
-    uint32_t k_first = 0, split = 0;
+    uint32_t k_first = 0, split = 0, part = 0;
     if (EPI == HK_EPI_PARTIAL) {
-        const uint32_t tiles = g.tiles_m * g.tiles_n;
-        split = pid / tiles;
-        pid -= split * tiles;
+        split = pid / g.part_tiles;
+        part = pid - split * g.part_tiles;
+        pid = g.tile_base + part;
         k_first = split * g.split_steps;
     }
-    const uint32_t band = HK_GROUP_M * g.tiles_n;
-    const uint32_t first_m = (pid / band) * HK_GROUP_M;
-    const uint32_t band_rows = min(g.tiles_m - first_m, (uint32_t)HK_GROUP_M);
-    const uint32_t in_band = pid % band;
-    const uint32_t tile_m = first_m + in_band % band_rows;
-    const uint32_t tile_n = in_band / band_rows;
+    uint32_t tile_m, tile_n;
+    hk_tile_coords(pid, g.tiles_m, g.tiles_n, tile_m, tile_n);
     const uint32_t m0 = tile_m * HK_BM;
 
     /* ---- staging plan ----
@@ -322,22 +333,20 @@ hk_gemm_mfma(hk_gemm_args g) {
      * one column group) and the row reads spread over the banks. */
     const uint32_t sub = frag_half * 4u;
     if (EPI == HK_EPI_PARTIAL) {
+        /* tile-local F32, whole tile (rows and columns past the matrix are
+         * zeros that the reduction skips) */
+        float *ptile = g.partial +
+                       ((size_t)split * g.part_tiles + part) * (HK_BM * HK_BN);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const uint32_t m = m0 + wm * 128u + j * 32u + frag_row;
-            if (m >= g.m) continue;
-            float *prow = g.partial + ((size_t)split * g.m + m) * g.n;
+            float *prow = ptile + (wm * 128u + j * 32u + frag_row) * HK_BN;
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const uint32_t col = tile_n * HK_BN + wn * 128u + i * 32u +
-                                         q * 8u + sub;
-                    if (col >= g.n) continue;
-                    *(float4 *)(prow + col) =
+                for (int q = 0; q < 4; q++)
+                    *(float4 *)(prow + wn * 128u + i * 32u + q * 8u + sub) =
                         make_float4(acc[i][j][q * 4], acc[i][j][q * 4 + 1],
                                     acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]);
-                }
         }
         return;
     }
@@ -523,31 +532,42 @@ __global__ void hk_swiglu_rows(const uint16_t *fused, uint16_t *out,
 
 static bool hk_gemm_lds_ready = false;
 
-/* Split-K reduction: C = bf16(sum_s partial[s] + bias), four columns per
- * thread (N % 4 == 0). */
-__global__ void hk_splitk_reduce(const float *__restrict__ partial,
-                                 const uint16_t *__restrict__ bias,
-                                 uint16_t *__restrict__ c, uint32_t m,
-                                 uint32_t n, uint32_t splits) {
-    const size_t quad = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const size_t count = (size_t)m * n;
-    if (quad * 4 >= count) return;
-    const size_t e = quad * 4;
-    float4 sum = *(const float4 *)(partial + e);
+/* Split-K reduction over the tile-local partials: 4 tile rows per
+ * workgroup, 4 columns per thread; C = epilogue(bf16 rounding of
+ * sum_s partial + bias), GELU after the reference's bf16 rounding. */
+template <int EPI>
+__global__ void __launch_bounds__(256)
+hk_splitk_reduce(hk_gemm_args g, uint32_t splits) {
+    const uint32_t part = blockIdx.x >> 6;
+    const uint32_t row = (blockIdx.x & 63u) * 4u + (threadIdx.x >> 6);
+    const uint32_t tcol = (threadIdx.x & 63u) * 4u;
+    uint32_t tile_m, tile_n;
+    hk_tile_coords(g.tile_base + part, g.tiles_m, g.tiles_n, tile_m, tile_n);
+    const uint32_t m = tile_m * HK_BM + row, n = tile_n * HK_BN + tcol;
+    if (m >= g.m || n >= g.n) return;
+    const size_t stride = (size_t)g.part_tiles * (HK_BM * HK_BN);
+    const float *p = g.partial + (size_t)part * (HK_BM * HK_BN) +
+                     row * HK_BN + tcol;
+    float4 sum = *(const float4 *)p;
     for (uint32_t s = 1; s < splits; s++) {
-        const float4 p = *(const float4 *)(partial + s * count + e);
-        sum.x += p.x; sum.y += p.y; sum.z += p.z; sum.w += p.w;
+        const float4 v = *(const float4 *)(p + s * stride);
+        sum.x += v.x; sum.y += v.y; sum.z += v.z; sum.w += v.w;
     }
-    if (bias) {
-        const uint32_t col = (uint32_t)(e % n);
-        const uint2 b = *(const uint2 *)(bias + col);
-        sum.x += hk_bf2f(b.x & 0xffffu);
-        sum.y += hk_bf2f(b.x >> 16);
-        sum.z += hk_bf2f(b.y & 0xffffu);
-        sum.w += hk_bf2f(b.y >> 16);
+    float out[4] = {sum.x, sum.y, sum.z, sum.w};
+    if (g.bias) {
+        const uint2 b = *(const uint2 *)(g.bias + n);
+        out[0] += hk_bf2f(b.x & 0xffffu);
+        out[1] += hk_bf2f(b.x >> 16);
+        out[2] += hk_bf2f(b.y & 0xffffu);
+        out[3] += hk_bf2f(b.y >> 16);
     }
-    *(uint2 *)(c + e) = make_uint2(hk_pack2(sum.x, sum.y),
-                                   hk_pack2(sum.z, sum.w));
+    if (EPI == HK_EPI_GELU) {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            out[e] = hk_gelu_tanh_f(hk_bf2f(hk_f2bf(out[e])));
+    }
+    *(uint2 *)(g.c + (size_t)m * g.n + n) =
+        make_uint2(hk_pack2(out[0], out[1]), hk_pack2(out[2], out[3]));
 }
 
 int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
@@ -594,31 +614,52 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
         g.w_bytes = (uint32_t)w_bytes;
         g.partial = NULL;
         g.split_steps = 0;
+        g.tile_base = 0;
+        g.part_tiles = 0;
         dim3 grid(g.tiles_m * g.tiles_n);
-        /* Split-K when the tiles would leave over half the CUs idle (the
-         * 512-row cross-attention K/V projections: 40 tiles): each of up to
-         * num_cus / tiles workgroups per tile takes at least 8 K steps, and
-         * a reduction adds the F32 partials, the bias and rounds. */
+        /* Split-K for a sparse last round: when the tiles left after the
+         * full rounds of one tile per CU (all of them, for small launches
+         * like the 512-row cross-attention K/V projections) would leave over
+         * half the CUs idle, those tiles are cut along K into up to
+         * num_cus / tiles pieces of at least 4 K steps each; a reduction
+         * adds the F32 partials, the bias and the activation. */
         const uint32_t tiles = g.tiles_m * g.tiles_n;
         const uint32_t k_steps = k / HK_BK;
         const uint32_t cus = gpu->num_cus > 0 ? (uint32_t)gpu->num_cus : 256u;
-        if (epilogue == HK_EPI_STORE && tiles * 2 <= cus && k_steps >= 16) {
-            uint32_t splits = min(cus / tiles, k_steps / 8);
+        const uint32_t full = tiles - tiles % cus, tail = tiles % cus;
+        if (epilogue != HK_EPI_SWIGLU && tail && tail * 2 <= cus &&
+            k_steps >= 8) {
+            uint32_t splits = min(cus / tail, k_steps / 4);
             const uint32_t steps = (k_steps + splits - 1) / splits;
             splits = (k_steps + steps - 1) / steps;
-            const size_t count = (size_t)m * n;
-            float *partial =
-                (float *)hk_splitk_space(gpu, (size_t)splits * count * 4);
+            float *partial = (float *)hk_splitk_space(
+                gpu, (size_t)splits * tail * HK_BM * HK_BN * 4);
             if (!partial) return 0;
+            if (full) {
+                if (epilogue == HK_EPI_GELU)
+                    hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_GELU>, dim3(full),
+                                       dim3(HK_GEMM_THREADS), HK_GEMM_LDS,
+                                       gpu->stream, g);
+                else
+                    hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_STORE>, dim3(full),
+                                       dim3(HK_GEMM_THREADS), HK_GEMM_LDS,
+                                       gpu->stream, g);
+            }
             g.partial = partial;
             g.split_steps = steps;
+            g.tile_base = full;
+            g.part_tiles = tail;
             hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_PARTIAL>,
-                               dim3(tiles * splits), dim3(HK_GEMM_THREADS),
+                               dim3(tail * splits), dim3(HK_GEMM_THREADS),
                                HK_GEMM_LDS, gpu->stream, g);
-            hipLaunchKernelGGL(hk_splitk_reduce,
-                               dim3((unsigned)((count / 4 + 255) / 256)),
-                               dim3(256), 0, gpu->stream, partial, bias, c, m,
-                               n, splits);
+            if (epilogue == HK_EPI_GELU)
+                hipLaunchKernelGGL(hk_splitk_reduce<HK_EPI_GELU>,
+                                   dim3(tail * 64), dim3(256), 0, gpu->stream,
+                                   g, splits);
+            else
+                hipLaunchKernelGGL(hk_splitk_reduce<HK_EPI_STORE>,
+                                   dim3(tail * 64), dim3(256), 0, gpu->stream,
+                                   g, splits);
             return 1;
         }
         if (epilogue == HK_EPI_SWIGLU)

@@ -42,6 +42,7 @@ def _mod_setup(rng, rows, width, slots=6, mod_rows=4):
     (512, 5120, 5120, True),    # split-K: Wan cross K/V projection (40 tiles)
     (260, 2048, 516, True),     # split-K, ragged M and N, 4 splits
     (600, 1088, 256, False),    # split-K with a short last split (17 steps)
+    (4096, 512, 4352, True),    # 272 tiles: one full round + a split tail
 ])
 def test_linear_bf16(gpu, m, k, n, bias):
     rng = np.random.default_rng(m * 7 + k + n)
@@ -79,6 +80,21 @@ def test_mlp_swiglu(gpu, rows, d, ffn):
     gpu.run("h3_gpu_mlp_bf16", out, gpu.bf16(x), gpu.bf16(fc1), gpu.bf16(fc2),
             rows, d, ffn, d)
     assert_close(gpu.read_bf16(out), want, what="SwiGLU MLP", chained=1)
+
+
+def test_linear_gelu_full_round_and_split_tail(gpu):
+    """272 tiles on 256 CUs: the first 256 run whole, the last 16 are cut
+    along K and reduced with the bias and GELU."""
+    m, k, n = 4096, 640, 4352
+    rng = np.random.default_rng(17)
+    x = rand_bf16(rng, m * k)
+    w = rand_bf16(rng, n * k, 0.05)
+    b = rand_bf16(rng, n, 0.1)
+    want = oracle.gelu(oracle.linear(x, w, b, m, k, n))
+    out = gpu.new_bf16(m * n)
+    gpu.run("h3_gpu_linear_gelu_bf16", out, gpu.bf16(x), gpu.bf16(w),
+            gpu.bf16(b), m, k, n)
+    assert_close(gpu.read_bf16(out), want, what="linear+GELU", chained=1)
 
 
 def test_ffn_gelu(gpu):
