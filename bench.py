@@ -76,7 +76,17 @@ def time_forward(gpu, dit, blocks, steps, warmup):
     return ms.value / steps, wall * 1000.0 / steps
 
 
-OPS_GEMM, OPS_ACT, OPS_ATTN, OPS_ROWS = 1, 2, 4, 8
+OPS_GEMM, OPS_ACT, OPS_ATTN, OPS_ROWS, OPS_CTX = 1, 2, 4, 8, 16
+
+
+KERNEL_NAMES = {
+    "gemm_plain": "hk_gemm_mfma<0> (QKV, out, cross q, cross out, FFN "
+                  "down)",
+    "gemm_gelu": "hk_gemm_mfma<2> + split tail (FFN up + GELU)",
+    "context_kv": "split-K hk_gemm_mfma<3> + reduce (cross K/V of the text)",
+    "attention": "hk_flash_fwd<false> (self + cross)",
+    "row_ops": "adaLN / gates / Q-K norm + RoPE / head norm / residual rows",
+}
 
 
 def class_replay(gpu, dit, blocks, mask, reps=2):
@@ -424,14 +434,15 @@ def main():
     cref = __import__("ctypes").byref(cfg)
     plain_flops = L.h3hip_dit_block_plain_gemm_flops(cref)
     plain_launches = L.h3hip_dit_block_plain_gemm_launches(cref)
-    gemm_ms = class_replay(gpu, dit, blocks, OPS_GEMM)
-    act_ms = class_replay(gpu, dit, blocks, OPS_ACT)
-    attn_ms = class_replay(gpu, dit, blocks, OPS_ATTN)
-    rows_ms = class_replay(gpu, dit, blocks, OPS_ROWS)
-    act_flops = gemm_flops - plain_flops
+    cls = {}
+    for name, mask in (("gemm_plain", OPS_GEMM), ("gemm_gelu", OPS_ACT),
+                       ("context_kv", OPS_CTX),
+                       ("attention", OPS_ATTN), ("row_ops", OPS_ROWS)):
+        ms = class_replay(gpu, dit, blocks, mask)
+        flops = L.h3hip_dit_block_class_flops(cref, mask)
+        cls[name] = (ms, flops)
+    gemm_ms = cls["gemm_plain"][0]
     gemm_tflops = blocks * plain_flops / (gemm_ms / 1e3) / 1e12
-    act_tflops = blocks * act_flops / (act_ms / 1e3) / 1e12
-    attn_tflops = blocks * attn_flops / (attn_ms / 1e3) / 1e12
     per_launch_flops = plain_flops / plain_launches
     per_launch_ms = gemm_ms / (blocks * plain_launches)
     dit.close()
@@ -482,25 +493,14 @@ def main():
         "mfma_util_pct": round(100 * total_tflops / BF16_PEAK_TFLOPS, 1),
         "wall_ms_per_step": round(wall_ms, 3),
         "kernels": {
-            "gemm_plain": {"kernel": "hk_gemm_mfma<0>",
-                           "tflops": round(gemm_tflops, 1),
-                           "frac_of_peak": round(gemm_tflops /
-                                                 BF16_PEAK_TFLOPS, 4),
-                           "launches_per_forward": blocks * plain_launches,
-                           "avg_launch_us": round(per_launch_ms * 1e3, 1),
-                           "ms_per_forward": round(gemm_ms, 3)},
-            "gemm_gelu": {"kernel": "hk_gemm_mfma<2>",
-                          "tflops": round(act_tflops, 1),
-                          "frac_of_peak": round(act_tflops /
-                                                BF16_PEAK_TFLOPS, 4),
-                          "ms_per_forward": round(act_ms, 3)},
-            "attention": {"kernel": "hk_flash_fwd",
-                          "tflops": round(attn_tflops, 1),
-                          "frac_of_peak": round(attn_tflops /
-                                                BF16_PEAK_TFLOPS, 4),
-                          "ms_per_forward": round(attn_ms, 3)},
-            "row_ops": {"ms_per_forward": round(rows_ms, 3)},
-        },
+            name: dict(
+                {"kernel": KERNEL_NAMES[name],
+                 "ms_per_forward": round(ms, 3)},
+                **({"tflops": round(blocks * fl / (ms / 1e3) / 1e12, 1),
+                    "frac_of_peak": round(blocks * fl / (ms / 1e3) / 1e12 /
+                                          BF16_PEAK_TFLOPS, 4)}
+                   if fl else {}))
+            for name, (ms, fl) in cls.items()},
         "roofline": {"kernel": "hk_gemm_mfma<0> (plain-epilogue GEMMs of "
                                "the forward)",
                      "bound": "mfma",

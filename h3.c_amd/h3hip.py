@@ -179,6 +179,12 @@ def lib():
         "h3hip_dit_block_plain_gemm_launches": (_U32,
                                                 [C.POINTER(DitConfig)]),
         "h3hip_dit_block_flops": (C.c_double, [C.POINTER(DitConfig)]),
+        "h3hip_dit_block_class_flops": (C.c_double,
+                                        [C.POINTER(DitConfig), C.c_uint]),
+        "h3_gpu_grouped_qkv_linear_rope_bf16": (_I, [_P, _P, _P, _P, _P, _P,
+                                                     _P, _P, _P, _P, _P,
+                                                     _U32, _U32, _U32, _U32,
+                                                     _U32, _F]),
         "h3hip_dit_block_gemm_flops": (C.c_double, [C.POINTER(DitConfig)]),
         "h3hip_dit_block_attention_flops": (C.c_double,
                                             [C.POINTER(DitConfig)]),

@@ -75,6 +75,7 @@ static int dit_op(h3hip_dit *dit, int ok, const char *what) {
 #define K_ACT H3HIP_OPS_GEMM_ACT
 #define K_ATTN H3HIP_OPS_ATTENTION
 #define K_ROWS H3HIP_OPS_ROWS
+#define K_CTX H3HIP_OPS_CONTEXT
 
 const char *h3hip_dit_error(const h3hip_dit *dit) {
     return dit ? dit->error : "no DiT";
@@ -415,8 +416,9 @@ static int run_h3_block(h3hip_dit *dit, uint32_t index, int fuse_next) {
                 "attention adaLN"))
         return 0;
     dit->attention_adaln_ready = 0;
-    /* h3_gpu_grouped_qkv_linear_rope_bf16 is exactly these two calls on
-     * this backend; issuing them separately keeps the op classes apart */
+    /* h3_gpu_grouped_qkv_linear_rope_bf16 (the reference engine's call,
+     * h3_dit.c:2046-2050) is exactly these two calls on this backend;
+     * issuing them separately keeps the op classes apart */
     if (!DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->qkv, dit->mod_a, w->qkv,
                                         NULL, rows, hidden, 3 * inner),
                 "QKV projection") ||
@@ -504,15 +506,15 @@ static int run_wan_block(h3hip_dit *dit, uint32_t index) {
                                                  w->cq_norm, rows, c->heads,
                                                  c->head_dim, eps),
                   "cross Q norm") &&
-           DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->cross_k, dit->context,
-                                          w->ck, w->ck_bias, t, d, inner),
+           DIT_OP(K_CTX, h3_gpu_linear_bf16(gpu, dit->cross_k, dit->context,
+                                         w->ck, w->ck_bias, t, d, inner),
                   "cross K projection") &&
            DIT_OP(K_ROWS, h3_gpu_head_rms_norm_bf16(gpu, dit->cross_k,
                                                  w->ck_norm, t, c->heads,
                                                  c->head_dim, eps),
                   "cross K norm") &&
-           DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->cross_v, dit->context,
-                                          w->cv, w->cv_bias, t, d, inner),
+           DIT_OP(K_CTX, h3_gpu_linear_bf16(gpu, dit->cross_v, dit->context,
+                                         w->cv, w->cv_bias, t, d, inner),
                   "cross V projection") &&
            DIT_OP(K_ATTN, h3_gpu_sdpa_cross_bf16(gpu, dit->cross_out,
                                               dit->cross_q, dit->cross_k,
@@ -548,19 +550,30 @@ int h3hip_dit_run_blocks(h3hip_dit *dit, uint32_t first, uint32_t count) {
     return h3hip_dit_run_blocks_ops(dit, first, count, H3HIP_OPS_ALL);
 }
 
-double h3hip_dit_block_plain_gemm_flops(const h3hip_dit_config *c) {
+double h3hip_dit_block_class_flops(const h3hip_dit_config *c,
+                                   unsigned op_class) {
     double d = c->hidden, inner = (double)c->heads * c->head_dim;
-    double n = c->rows, f = c->ffn;
-    if (c->family == H3HIP_FAMILY_WAN)
-        /* qkv, out, cross q, cross out, ffn down; cross k, v on the text */
-        return 2.0 * n * (3 * d * inner + 3 * inner * d + f * d) +
-               2.0 * c->text_rows * (2 * d * inner);
-    /* qkv, out (the SwiGLU MLP is one class-ACT op) */
-    return 2.0 * n * (3 * d * inner + inner * d);
+    double n = c->rows, f = c->ffn, t = c->text_rows;
+    const int wan = c->family == H3HIP_FAMILY_WAN;
+    switch (op_class) {
+    case H3HIP_OPS_GEMM:
+        /* QKV, out (+ Wan: cross q, cross out, FFN down) */
+        return wan ? 2.0 * n * (3 * d * inner + 3 * d * inner + f * d)
+                   : 2.0 * n * (3 * d * inner + inner * d);
+    case H3HIP_OPS_CONTEXT: return wan ? 2.0 * t * 2 * d * inner : 0.0;
+    case H3HIP_OPS_GEMM_ACT:
+        return wan ? 2.0 * n * d * f : 2.0 * n * (2 * f * d + f * d);
+    case H3HIP_OPS_ATTENTION: return h3hip_dit_block_attention_flops(c);
+    default: return 0.0;
+    }
+}
+
+double h3hip_dit_block_plain_gemm_flops(const h3hip_dit_config *c) {
+    return h3hip_dit_block_class_flops(c, H3HIP_OPS_GEMM);
 }
 
 uint32_t h3hip_dit_block_plain_gemm_launches(const h3hip_dit_config *c) {
-    return c->family == H3HIP_FAMILY_WAN ? 7u : 2u;
+    return c->family == H3HIP_FAMILY_WAN ? 5u : 2u;
 }
 
 int h3hip_dit_run_blocks_ops(h3hip_dit *dit, uint32_t first, uint32_t count,

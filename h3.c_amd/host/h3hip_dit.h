@@ -93,16 +93,23 @@ int h3hip_dit_run_blocks(h3hip_dit *dit, uint32_t first, uint32_t count);
  * order and with the same shapes and tensors as run_blocks() (the numerics
  * of a partial run are meaningless; the launches are identical). */
 enum {
-    H3HIP_OPS_GEMM = 1,      /* plain-epilogue projections (+bias) */
+    H3HIP_OPS_GEMM = 1,      /* plain-epilogue projections (+bias) over the
+                                sequence rows */
     H3HIP_OPS_GEMM_ACT = 2,  /* projections with a SwiGLU / GELU epilogue */
     H3HIP_OPS_ATTENTION = 4, /* flash attention (self and cross) */
     H3HIP_OPS_ROWS = 8,      /* adaLN, gates, norms, RoPE, residual adds */
-    H3HIP_OPS_ALL = 15
+    H3HIP_OPS_CONTEXT = 16,  /* Wan: cross K / V projections of the text */
+    H3HIP_OPS_ALL = 31
 };
 int h3hip_dit_run_blocks_ops(h3hip_dit *dit, uint32_t first, uint32_t count,
                              unsigned op_mask);
 /* FLOPs one block spends in the plain-epilogue projections (class GEMM). */
 double h3hip_dit_block_plain_gemm_flops(const h3hip_dit_config *config);
+/* FLOPs one block spends in the ops of one class (a single H3HIP_OPS_ bit;
+ * GEMM FLOPs for the projection classes, QK^T and PV for attention, 0 for
+ * the row ops). */
+double h3hip_dit_block_class_flops(const h3hip_dit_config *config,
+                                   unsigned op_class);
 /* Launches of class GEMM per block. */
 uint32_t h3hip_dit_block_plain_gemm_launches(const h3hip_dit_config *config);
 

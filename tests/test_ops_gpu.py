@@ -433,3 +433,4 @@ def test_validation_errors(gpu):
 def test_int8_paths_report_unavailable(gpu):
     assert gpu.L.h3_gpu_has_int8_mlp(gpu.h) == 0
     assert gpu.L.h3_gpu_prefers_gpu_sampler(gpu.h) == 1
+
