@@ -282,9 +282,7 @@ __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
 #pragma unroll
                 for (int r = 0; r < 16; r += 2)
                     mx = __builtin_fmaxf(
-                        mx, __builtin_amdgcn_fmed3f(s[kt][g][r],
-                                                    s[kt][g][r + 1],
-                                                    __builtin_inff()));
+                        mx, __builtin_fmaxf(s[kt][g][r], s[kt][g][r + 1]));
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * a.scale_log2;
             const bool grow = mx > m_run[g] + 8.0f;
             if (__builtin_amdgcn_ballot_w64(grow)) {
