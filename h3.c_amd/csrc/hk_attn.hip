@@ -42,6 +42,8 @@
 #include "hk_internal.h"
 
 #include <math.h>
+#include <stdlib.h>
+#include <string.h>
 #include <type_traits>
 
 #define HK_HD 128
@@ -449,7 +451,14 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
     if (!q_rows || !heads) return 1;
     const uint64_t q_bytes = (uint64_t)q_rows * heads * head_dim * 2;
     const uint64_t kv_bytes = (uint64_t)kv_rows * heads * head_dim * 2;
-    const bool flash = !gpu->reference_kernels && head_dim == HK_HD &&
+    /* the reference's debugging knob H3_CUDA_SDPA_NAIVE=1 (read per call,
+     * like its backend: h3_cuda_attention.cu) selects the two-pass kernel;
+     * H3_HIP_SDPA_NAIVE is the same knob under this backend's prefix */
+    const char *naive = getenv("H3_CUDA_SDPA_NAIVE");
+    if (!naive || !*naive) naive = getenv("H3_HIP_SDPA_NAIVE");
+    const bool naive_on = naive && *naive && strcmp(naive, "0") != 0;
+    const bool flash = !gpu->reference_kernels && !naive_on &&
+                       head_dim == HK_HD &&
                        kv_rows > 0 && q_bytes < 0xfffff000ull &&
                        kv_bytes < 0xfffff000ull &&
                        ((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0 &&

@@ -151,6 +151,8 @@ def lib():
         "h3_gpu_adaln_linear_bf16": (_I, [_P, _P, _P, _P, _SZ, _P, _P, _P,
                                           _P, _P, _U32, _U32, _U32, _U32,
                                           _U32, _U32, _F]),
+        "h3_hip_patch_linear_bf16_offset": (_I, [_P, _P, _SZ, _P, _SZ, _P, _P,
+                                                 _U32, _U32, _U32]),
         "h3_gpu_patch_linear_bf16_offset": (_I, [_P, _P, _SZ, _P, _SZ, _P, _P,
                                                  _U32, _U32, _U32]),
         "h3_gpu_patch_linear_bf16_map": (_I, [_P, _P, _P, _P, _P, _P, _U32,

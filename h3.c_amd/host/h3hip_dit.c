@@ -620,6 +620,24 @@ static void sampler_free(h3hip_dit *dit) {
     free(dit->segments);
 }
 
+/* The engine's own patch projection takes only the checkpoint shapes
+ * (5376 outputs from 96 / 32 inputs); reduced-width test models use the
+ * shape-generic variant of the same op. */
+static int patch_offset(h3_gpu *gpu, h3_gpu_tensor *output,
+                        size_t output_offset, const h3_gpu_tensor *input,
+                        size_t input_offset, const h3_gpu_tensor *weight,
+                        const h3_gpu_tensor *bias, uint32_t rows,
+                        uint32_t input_dim, uint32_t output_dim) {
+    if (output_dim == 5376 && (input_dim == 32 || input_dim == 96))
+        return h3_gpu_patch_linear_bf16_offset(gpu, output, output_offset,
+                                               input, input_offset, weight,
+                                               bias, rows, input_dim,
+                                               output_dim);
+    return h3_hip_patch_linear_bf16_offset(gpu, output, output_offset, input,
+                                           input_offset, weight, bias, rows,
+                                           input_dim, output_dim);
+}
+
 static int is_video_kind(int kind) {
     return kind == H3HIP_SEG_COND || kind == H3HIP_SEG_REF_IMAGE ||
            kind == H3HIP_SEG_VIDEO;
@@ -903,7 +921,7 @@ int h3hip_dit_forward_step(h3hip_dit *dit, int step) {
                         "pack refined text");
             text_offset += n;
         } else if (is_video_kind(seg->kind)) {
-            ok = dit_op(dit, h3_gpu_patch_linear_bf16_offset(
+            ok = dit_op(dit, patch_offset(
                                  gpu, dit->hidden, destination,
                                  dit->video_input,
                                  video_offset * dit->video_patch,
@@ -912,7 +930,7 @@ int h3hip_dit_forward_step(h3hip_dit *dit, int step) {
                         "project packed video source");
             video_offset += n;
         } else {
-            ok = dit_op(dit, h3_gpu_patch_linear_bf16_offset(
+            ok = dit_op(dit, patch_offset(
                                  gpu, dit->hidden, destination,
                                  dit->audio_input,
                                  audio_offset * dit->audio_channels,

@@ -66,6 +66,24 @@ int h3_gpu_layer_adaln_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
 
 /* output = bf16(gelu_tanh(bf16(X . W^T + b))): GEMM with the activation in
  * its epilogue. */
+/* h3_gpu_patch_linear_bf16_offset / _map (h3_gpu.h:116-135) without the
+ * reference's fixed checkpoint shape (5376 outputs from 32 or 96 inputs):
+ * any output width and up to 4096 inputs, for reduced-width test models.
+ * The h3_gpu_ entries keep the reference's check. */
+int h3_hip_patch_linear_bf16_offset(h3_gpu *gpu, h3_gpu_tensor *output,
+                                    size_t output_offset,
+                                    const h3_gpu_tensor *input,
+                                    size_t input_offset,
+                                    const h3_gpu_tensor *weight,
+                                    const h3_gpu_tensor *bias, uint32_t rows,
+                                    uint32_t input_dim, uint32_t output_dim);
+int h3_hip_patch_linear_bf16_map(h3_gpu *gpu, h3_gpu_tensor *output,
+                                 const h3_gpu_tensor *input,
+                                 const h3_gpu_tensor *weight,
+                                 const h3_gpu_tensor *bias,
+                                 const h3_gpu_tensor *row_map,
+                                 uint32_t output_rows, uint32_t rows,
+                                 uint32_t input_dim, uint32_t output_dim);
 int h3_gpu_linear_gelu_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
                             const h3_gpu_tensor *input,
                             const h3_gpu_tensor *weight,

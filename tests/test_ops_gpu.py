@@ -400,6 +400,28 @@ def test_patch_linear_bit_exact(gpu):
     assert_ulp(gpu.read_bf16(out), want, 0, "mapped patch projection")
 
 
+def test_patch_linear_shapes(gpu):
+    """The h3_gpu_ entries accept only the checkpoint shapes (5376 outputs
+    from 32 or 96 inputs, h3_cuda_core.cu:929-930; the reference's own test
+    tests/test_cuda_core.c:890-894); the h3_hip_ variant takes a reduced
+    width, bit-exact against the oracle."""
+    rows, k, n = 12, 96, 256
+    rng = np.random.default_rng(14)
+    x = rng.standard_normal(rows * k).astype(np.float32)
+    w = (0.05 * rng.standard_normal(n * k)).astype(np.float32)
+    out = gpu.new_bf16(rows * n)
+    tx, tw = gpu.f32(x), gpu.f32(w)
+    gpu.begin()
+    assert not gpu.L.h3_gpu_patch_linear_bf16_offset(gpu.h, out, 0, tx, 0, tw,
+                                                      None, rows, k, n)
+    assert "unsupported fused patch projection shape" in gpu.error()
+    gpu.submit()
+    gpu.run("h3_hip_patch_linear_bf16_offset", out, 0, tx, 0, tw, None, rows,
+            k, n)
+    want = oracle.patch_linear(x, w, None, rows, k, n)
+    assert_ulp(gpu.read_bf16(out), want, 0, "reduced-width patch projection")
+
+
 # ------------------------------------------------------------ contract
 
 def test_ops_require_an_open_batch(gpu):
