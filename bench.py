@@ -131,18 +131,20 @@ def profile_pass(gpu, dit, blocks):
     log("profile pass done")
 
 
-def h3_measure(gpu, blocks, reps):
-    """The H3 block at its real 512x512x22f shape (512 text + 74 audio +
-    1792 video rows): one 50-block forward, and BASELINE config 5, the
-    20-step serving-schedule Euler denoise with velocity reuse 2 (11 fresh
-    forwards, extrapolated skipped steps), end to end on the GPU: patch
-    projection, packing, blocks, final adaLN heads, Euler updates."""
+def h3_measure(gpu, blocks, reps, latent_h=32, latent_w=32, full=True):
+    """The H3 block at a real shape (512 text + 74 audio + video rows of a
+    22-frame latent_h x latent_w latent: 2378 rows at 512x512, 3421 at
+    864x480): one 50-block forward and, with full=True, the documented
+    sparse window and BASELINE config 5, the 20-step serving-schedule Euler
+    denoise with velocity reuse 2 (11 fresh forwards, extrapolated skipped
+    steps), end to end on the GPU: patch projection, packing, blocks, final
+    adaLN heads, Euler updates."""
     import ctypes as C
     L = h3hip.lib()
     lay = h3hip.Layout()
     err = C.create_string_buffer(256)
-    if not L.h3hip_layout_build(512, 7, 32, 32, 37, 22, None, 0, None, 0,
-                                C.byref(lay), err, 256):
+    if not L.h3hip_layout_build(512, 7, latent_h, latent_w, 37, 22, None, 0,
+                                None, 0, C.byref(lay), err, 256):
         raise RuntimeError(err.value.decode())
     n = lay.seq_len
     pos = np.array([[lay.positions[i].t, lay.positions[i].h,
@@ -180,6 +182,8 @@ def h3_measure(gpu, blocks, reps):
         real = {"rows": int(n), "s_per_forward": round(hms / 1e3, 4),
                 "ms_per_block": round(hms / blocks, 3),
                 "tflops": round(blocks * hflops / (hms / 1e3) / 1e12, 1)}
+        if not full:
+            return real, None
         # the reference's documented block-sparse window (README H3_SPARSE_ATTN
         # =16:8:14:8): forward time with the mask, then back to dense
         kept = L.h3hip_dit_set_sparse_window(hdit.h, C.byref(lay), 16, 8, 14,
@@ -453,11 +457,14 @@ def main():
         sweep = attention_sweep(gpu)
         wan_big = wan_864x480(gpu, blocks, max(2, args.steps // 2))
 
-    h3_real = None
+    h3_real = h3_big = None
     denoise = None
     if not args.no_h3 and not args.no_extras:
         log("H3 real shape: forward + 20-step Euler denoise ...")
         h3_real, denoise = h3_measure(gpu, blocks, max(2, args.steps // 2))
+        log("H3 864x480 forward ...")
+        h3_big, _ = h3_measure(gpu, blocks, max(2, args.steps // 2),
+                               latent_h=30, latent_w=54, full=False)
 
     if not args.no_extras:
         log("weight file loading ...")
@@ -513,6 +520,7 @@ def main():
                      "avg_launch_us": round(per_launch_ms * 1e3, 1),
                      "traffic": load_traffic("gemm_plain_wan512_traffic.json")},
         "h3_real_shape": h3_real,
+        "h3_864x480": h3_big,
         "denoise": denoise,
         "attention_sweep": sweep,
         "wan_864x480": wan_big,
