@@ -124,7 +124,10 @@ __attribute__((amdgpu_waves_per_eu(1, 1)))
 hk_gemm_mfma(hk_gemm_args g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t hk_smem[];
     const uint32_t tid = threadIdx.x;
-    const uint32_t lane = tid & 63, wave = tid >> 6;
+    /* the wave index is uniform: keep it (and the LDS destinations of the
+     * DMA loads derived from it) in scalar registers */
+    const uint32_t lane = tid & 63,
+                   wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = wave & 1, wn = wave >> 1;
 
     /* ---- workgroup -> tile (XCD regroup, then GROUP_M bands) ---- */
@@ -186,16 +189,18 @@ hk_gemm_mfma(hk_gemm_args g) {
         uint8_t *sx = hk_smem + stage * HK_STAGE_BYTES;
         const int j = t >> 1;
         const uint32_t base = (wave * 8u + j) * 1024u;
+        /* the stage's k offset goes in the scalar offset: rows past the
+         * matrix keep a lane offset beyond the buffer and still read 0 */
         if ((t & 1) == 0)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 xr, (__attribute__((address_space(3))) void *)(sx + base), 16,
-                x_off[j] + kb, 0, 0, 0);
+                x_off[j], kb, 0, 0);
         else
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 wr,
                 (__attribute__((address_space(3))) void *)(sx + HK_TILE_BYTES +
                                                            base),
-                16, w_off[j] + kb, 0, 0, 0);
+                16, w_off[j], kb, 0, 0);
     };
     auto issue_loads = [&](uint32_t stage, uint32_t k0) {
 #pragma unroll
