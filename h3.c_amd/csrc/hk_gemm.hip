@@ -417,17 +417,26 @@ hk_gemm_mfma(hk_gemm_args g) {
     constexpr uint32_t rows_per_pass = HK_GEMM_THREADS / chunks;
     const uint32_t chunk = tid % chunks;
     const uint32_t col = n0 + chunk * 8u;
-#pragma unroll 4
-    for (uint32_t row = tid / chunks; row < HK_BM; row += rows_per_pass) {
-        const uint32_t m = m0 + row;
-        if (m >= g.m || col >= g.n) continue;
-        const uint8_t *src = hk_smem + row * pitch +
-                             ((chunk ^ (row & (chunks - 1u))) << 4);
-        uint16_t *dst = g.c + (size_t)m * g.n + col;
-        if (col + 8u <= g.n)
-            *(uint4 *)dst = *(const uint4 *)src;
-        else
-            *(uint2 *)dst = *(const uint2 *)src;
+    /* eight LDS reads in flight before their stores */
+    for (uint32_t row0 = tid / chunks; row0 < HK_BM;
+         row0 += 8u * rows_per_pass) {
+        uint4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const uint32_t row = row0 + u * rows_per_pass;
+            v[u] = *(const uint4 *)(hk_smem + row * pitch +
+                                    ((chunk ^ (row & (chunks - 1u))) << 4));
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const uint32_t m = m0 + row0 + u * rows_per_pass;
+            if (m >= g.m || col >= g.n) continue;
+            uint16_t *dst = g.c + (size_t)m * g.n + col;
+            if (col + 8u <= g.n)
+                *(uint4 *)dst = v[u];
+            else
+                *(uint2 *)dst = make_uint2(v[u].x, v[u].y);
+        }
     }
 }
 
