@@ -345,10 +345,71 @@ __global__ void hk_elementwise(const void *left, const void *right, void *out,
     }
 }
 
+/* bf16 -> bf16 ops, 8 elements (16 bytes) per thread and step; the last
+ * count % 8 elements go to the first threads of the grid. */
+template <int OP>
+__device__ __forceinline__ float hk_ew_bf16(float x, float y) {
+    if (OP == HK_EW_SILU_BF16) return hk_silu(x);
+    if (OP == HK_EW_GELU_TANH) return hk_gelu_tanh(x);
+    if (OP == HK_EW_GELU_ERF) return hk_gelu_erf(x);
+    if (OP == HK_EW_ADD_BF16) return x + y;
+    if (OP == HK_EW_SUB_BF16) return x - y;
+    return hk_silu(x) * y; /* HK_EW_SILU_MUL_BF16 */
+}
+
+template <int OP>
+__global__ void __launch_bounds__(256)
+hk_elementwise8(const uint16_t *left, const uint16_t *right, uint16_t *out,
+                size_t count) {
+    constexpr bool binary = OP == HK_EW_ADD_BF16 || OP == HK_EW_SUB_BF16 ||
+                            OP == HK_EW_SILU_MUL_BF16;
+    const size_t chunks = count / 8;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    const size_t first = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (size_t c = first; c < chunks; c += stride) {
+        const uint4 a = ((const uint4 *)left)[c];
+        uint4 b = make_uint4(0, 0, 0, 0);
+        if (binary) b = ((const uint4 *)right)[c];
+        const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
+        const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
+        uint32_t ow[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            ow[e] = hk_pack2(
+                hk_ew_bf16<OP>(hk_bf2f(aw[e] & 0xffffu),
+                               hk_bf2f(bw[e] & 0xffffu)),
+                hk_ew_bf16<OP>(hk_bf2f(aw[e] >> 16), hk_bf2f(bw[e] >> 16)));
+        ((uint4 *)out)[c] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+    }
+    const size_t tail = chunks * 8 + first;
+    if (tail < count)
+        out[tail] = hk_f2bf(
+            hk_ew_bf16<OP>(hk_bf2f(left[tail]),
+                           binary ? hk_bf2f(right[tail]) : 0.0f));
+}
+
 template <int OP>
 static void hk_ew_launch(struct h3_gpu *gpu, const void *left,
                          const void *right, void *out, size_t count) {
     if (!count) return;
+    constexpr bool bf16_out = OP == HK_EW_SILU_BF16 ||
+                              OP == HK_EW_GELU_TANH ||
+                              OP == HK_EW_GELU_ERF || OP == HK_EW_ADD_BF16 ||
+                              OP == HK_EW_SUB_BF16 ||
+                              OP == HK_EW_SILU_MUL_BF16;
+    const uintptr_t bases = (uintptr_t)left | (uintptr_t)right |
+                            (uintptr_t)out;
+    if (bf16_out && (bases & 15u) == 0) {
+        size_t blocks = (count / 8 + 255) / 256;
+        const size_t cap = (size_t)gpu->num_cus * 8;
+        if (blocks > cap) blocks = cap;
+        if (blocks == 0) blocks = 1;
+        hipLaunchKernelGGL(hk_elementwise8<OP>, dim3((unsigned)blocks),
+                           dim3(256), 0, gpu->stream,
+                           (const uint16_t *)left, (const uint16_t *)right,
+                           (uint16_t *)out, count);
+        return;
+    }
     size_t blocks = (count + 255) / 256;
     size_t cap = (size_t)gpu->num_cus * 16;
     if (blocks > cap) blocks = cap;
@@ -467,6 +528,131 @@ hk_qk_norm_rope128(const uint16_t *__restrict__ qkv,
     *(uint32_t *)(value + out) = vr;
 }
 
+/* The same with DPL dims (2·DPL bytes) per lane and 128 / DPL lanes per
+ * (row, head), for rope_half % DPL == 0: the dims of a lane then sit on one
+ * side of the rotate-half split and their partners rope_half / DPL lanes
+ * away. */
+template <int DPL> struct hk_vec_of;
+template <> struct hk_vec_of<4> { typedef uint2 type; };
+template <> struct hk_vec_of<8> { typedef uint4 type; };
+
+template <int DPL>
+__device__ __forceinline__ void hk_unpack(const uint16_t *p, float v[DPL]) {
+    const typename hk_vec_of<DPL>::type raw =
+        *(const typename hk_vec_of<DPL>::type *)p;
+    const uint32_t *w = (const uint32_t *)&raw;
+#pragma unroll
+    for (int e = 0; e < DPL / 2; e++) {
+        v[2 * e] = hk_bf2f(w[e] & 0xffffu);
+        v[2 * e + 1] = hk_bf2f(w[e] >> 16);
+    }
+}
+
+template <int DPL>
+__device__ __forceinline__ void hk_pack_store(uint16_t *p, const float v[DPL]) {
+    typename hk_vec_of<DPL>::type raw;
+    uint32_t *w = (uint32_t *)&raw;
+#pragma unroll
+    for (int e = 0; e < DPL / 2; e++) w[e] = hk_pack2(v[2 * e], v[2 * e + 1]);
+    *(typename hk_vec_of<DPL>::type *)p = raw;
+}
+
+template <int DPL>
+__global__ void __launch_bounds__(256)
+hk_qk_norm_rope128v(const uint16_t *__restrict__ qkv,
+                    const uint16_t *__restrict__ q_weight,
+                    const uint16_t *__restrict__ k_weight,
+                    const uint16_t *__restrict__ rope_cos,
+                    const uint16_t *__restrict__ rope_sin,
+                    uint16_t *__restrict__ query, uint16_t *__restrict__ key,
+                    uint16_t *__restrict__ value, uint32_t sequence,
+                    uint32_t heads, uint32_t rope_half, uint32_t grouped,
+                    float epsilon) {
+    constexpr uint32_t HD = 128, LANES = HD / DPL;
+    typedef typename hk_vec_of<DPL>::type vec_t;
+    const uint32_t vec = (blockIdx.x * blockDim.x + threadIdx.x) / LANES;
+    const uint32_t part = threadIdx.x % LANES;
+    const bool live = vec < sequence * heads;
+    const uint32_t row = live ? vec / heads : 0, head = live ? vec % heads : 0;
+    const size_t inner = (size_t)heads * HD;
+    const size_t row_base = (size_t)row * inner * 3;
+    size_t q_base, k_base, v_base;
+    if (grouped) {
+        q_base = row_base + (size_t)head * HD * 3;
+        k_base = q_base + HD;
+        v_base = k_base + HD;
+    } else {
+        q_base = row_base + (size_t)head * HD;
+        k_base = q_base + inner;
+        v_base = k_base + inner;
+    }
+    const uint32_t d0 = part * DPL;
+    float q[DPL], k[DPL], qw[DPL], kw[DPL];
+    hk_unpack<DPL>(qkv + q_base + d0, q);
+    hk_unpack<DPL>(qkv + k_base + d0, k);
+    const vec_t vr = *(const vec_t *)(qkv + v_base + d0);
+    hk_unpack<DPL>(q_weight + d0, qw);
+    hk_unpack<DPL>(k_weight + d0, kw);
+    float q_sum = 0.0f, k_sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < DPL; e++) {
+        q_sum = fmaf(q[e], q[e], q_sum);
+        k_sum = fmaf(k[e], k[e], k_sum);
+    }
+#pragma unroll
+    for (int offset = LANES / 2; offset; offset >>= 1) {
+        q_sum += __shfl_xor(q_sum, offset, LANES);
+        k_sum += __shfl_xor(k_sum, offset, LANES);
+    }
+    const float q_inv = 1.0f / sqrtf(q_sum / (float)HD + epsilon);
+    const float k_inv = 1.0f / sqrtf(k_sum / (float)HD + epsilon);
+    float qn[DPL], kn[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; e++) {
+        qn[e] = q[e] * q_inv * qw[e];
+        kn[e] = k[e] * k_inv * kw[e];
+    }
+    const uint32_t shift = rope_half / DPL;
+    int src = (int)part;
+    if (d0 < rope_half) src = (int)(part + shift);
+    else if (d0 < rope_half * 2) src = (int)(part - shift);
+    float qp[DPL], kp[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; e++) {
+        qp[e] = __shfl(qn[e], src, LANES);
+        kp[e] = __shfl(kn[e], src, LANES);
+    }
+    if (!live) return;
+    float qo[DPL], ko[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; e++) {
+        qo[e] = qn[e];
+        ko[e] = kn[e];
+    }
+    if (d0 < rope_half * 2) {
+        const bool first = d0 < rope_half;
+        const uint32_t pair = first ? d0 : d0 - rope_half;
+        const size_t table = (size_t)row * rope_half + pair;
+        float c[DPL], sn[DPL];
+        hk_unpack<DPL>(rope_cos + table, c);
+        hk_unpack<DPL>(rope_sin + table, sn);
+#pragma unroll
+        for (int e = 0; e < DPL; e++) {
+            if (first) {
+                qo[e] = qn[e] * c[e] - qp[e] * sn[e];
+                ko[e] = kn[e] * c[e] - kp[e] * sn[e];
+            } else {
+                qo[e] = qn[e] * c[e] + qp[e] * sn[e];
+                ko[e] = kn[e] * c[e] + kp[e] * sn[e];
+            }
+        }
+    }
+    const size_t out = ((size_t)row * heads + head) * HD + d0;
+    hk_pack_store<DPL>(query + out, qo);
+    hk_pack_store<DPL>(key + out, ko);
+    *(vec_t *)(value + out) = vr;
+}
+
 /* Generic per-element variant for other head sizes (any rope_half with
  * 2*rope_half <= head_dim). */
 template <typename T>
@@ -561,6 +747,39 @@ hk_head_rms_kernel(uint16_t *tensor, const uint16_t *weight,
         1.0f / sqrtf(hk_wave_sum(sum) / (float)head_dim + epsilon);
     for (uint32_t d = lane; d < head_dim; d += 64)
         x[d] = hk_f2bf(hk_bf2f(x[d]) * inverse * hk_bf2f(weight[d]));
+}
+
+/* The same for head_dim 128: 16 lanes per (row, head), 8 dims (16 bytes)
+ * per lane, four heads per wave. */
+__global__ void __launch_bounds__(256)
+hk_head_rms128(uint16_t *tensor, const uint16_t *weight, uint32_t vectors,
+               float epsilon) {
+    const uint32_t vec = (blockIdx.x * blockDim.x + threadIdx.x) >> 4;
+    const uint32_t part = threadIdx.x & 15u;
+    const bool live = vec < vectors;
+    uint4 *x = (uint4 *)(tensor + (size_t)(live ? vec : 0) * 128u) + part;
+    const uint4 raw = live ? *x : make_uint4(0, 0, 0, 0);
+    const uint4 wraw = ((const uint4 *)weight)[part];
+    const uint32_t xw[4] = {raw.x, raw.y, raw.z, raw.w};
+    const uint32_t ww[4] = {wraw.x, wraw.y, wraw.z, wraw.w};
+    float v[8], sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        v[2 * e] = hk_bf2f(xw[e] & 0xffffu);
+        v[2 * e + 1] = hk_bf2f(xw[e] >> 16);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e++) sum = fmaf(v[e], v[e], sum);
+#pragma unroll
+    for (int offset = 8; offset; offset >>= 1)
+        sum += __shfl_xor(sum, offset, 16);
+    const float inverse = 1.0f / sqrtf(sum / 128.0f + epsilon);
+    uint32_t ow[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        ow[e] = hk_pack2(v[2 * e] * inverse * hk_bf2f(ww[e] & 0xffffu),
+                         v[2 * e + 1] * inverse * hk_bf2f(ww[e] >> 16));
+    if (live) *x = make_uint4(ow[0], ow[1], ow[2], ow[3]);
 }
 
 /* ------------------------------------------------- small projections */
@@ -1371,7 +1590,30 @@ static int hk_qkv_rope(h3_gpu *gpu, h3_gpu_tensor *query, h3_gpu_tensor *key,
     const char *name = grouped ? "qk_norm_rope_grouped" : "qk_norm_rope";
     hk_op_begin(gpu, name);
     if (count) {
-        if (head_dim == 128 && rope_half % 2 == 0) {
+        const uintptr_t bases =
+            (uintptr_t)qkv->data | (uintptr_t)q_norm->data |
+            (uintptr_t)k_norm->data | (uintptr_t)rope_cos->data |
+            (uintptr_t)rope_sin->data | (uintptr_t)query->data |
+            (uintptr_t)key->data | (uintptr_t)value->data;
+        const size_t vectors = (size_t)sequence * heads;
+        if (head_dim == 128 && rope_half % 8 == 0 && (bases & 15u) == 0) {
+            hipLaunchKernelGGL(hk_qk_norm_rope128v<8>,
+                               dim3((unsigned)((vectors + 15) / 16)),
+                               dim3(256), 0, gpu->stream, HK_CBF16(qkv),
+                               HK_CBF16(q_norm), HK_CBF16(k_norm),
+                               HK_CBF16(rope_cos), HK_CBF16(rope_sin),
+                               HK_BF16(query), HK_BF16(key), HK_BF16(value),
+                               sequence, heads, rope_half, grouped, epsilon);
+        } else if (head_dim == 128 && rope_half % 4 == 0 &&
+                   (bases & 7u) == 0) {
+            hipLaunchKernelGGL(hk_qk_norm_rope128v<4>,
+                               dim3((unsigned)((vectors + 7) / 8)), dim3(256),
+                               0, gpu->stream, HK_CBF16(qkv), HK_CBF16(q_norm),
+                               HK_CBF16(k_norm), HK_CBF16(rope_cos),
+                               HK_CBF16(rope_sin), HK_BF16(query),
+                               HK_BF16(key), HK_BF16(value), sequence, heads,
+                               rope_half, grouped, epsilon);
+        } else if (head_dim == 128 && rope_half % 2 == 0) {
             size_t waves = (size_t)sequence * heads;
             hipLaunchKernelGGL(hk_qk_norm_rope128,
                                dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
@@ -1465,7 +1707,14 @@ int h3_gpu_head_rms_norm_bf16(h3_gpu *gpu, h3_gpu_tensor *tensor,
         return 0;
     hk_op_begin(gpu, "head_rms_norm");
     size_t waves = (size_t)sequence * heads;
-    if (count)
+    const bool wide = head_dim == 128 &&
+                      (((uintptr_t)tensor->data | (uintptr_t)weight->data) &
+                       15u) == 0;
+    if (count && wide)
+        hipLaunchKernelGGL(hk_head_rms128, dim3((unsigned)((waves + 15) / 16)),
+                           dim3(256), 0, gpu->stream, HK_BF16(tensor),
+                           HK_CBF16(weight), (uint32_t)waves, epsilon);
+    else if (count)
         hipLaunchKernelGGL(hk_head_rms_kernel,
                            dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
                            gpu->stream, HK_BF16(tensor), HK_CBF16(weight),

@@ -237,8 +237,9 @@ def test_rms_norm(gpu, width):
                                  1e-5), "RMS norm")
 
 
-def test_head_rms_norm(gpu):
-    rows, heads, hd = 33, 5, 128
+@pytest.mark.parametrize("hd", [128, 64])
+def test_head_rms_norm(gpu, hd):
+    rows, heads = 33, 5
     rng = np.random.default_rng(11)
     x, w = rand_bf16(rng, rows * heads * hd), rand_bf16(rng, hd, 0.1, 1.0)
     want = oracle.head_rms_norm(x, w, rows, heads, hd, 1e-6)
@@ -249,7 +250,8 @@ def test_head_rms_norm(gpu):
 
 
 @pytest.mark.parametrize("grouped", [True, False])
-@pytest.mark.parametrize("hd,rope_half", [(128, 48), (64, 16)])
+@pytest.mark.parametrize("hd,rope_half", [(128, 48), (128, 64), (128, 52),
+                                          (128, 46), (64, 16)])
 def test_qkv_rope(gpu, grouped, hd, rope_half):
     seq, heads = 45, 3
     rng = np.random.default_rng(hd + rope_half + grouped)
@@ -349,6 +351,11 @@ def test_swiglu_gelu_add_sub(gpu):
     y = rand_bf16(rng, 5000)
     gpu.run("h3_gpu_add_bf16", out, gpu.bf16(x), gpu.bf16(y), x.size)
     assert_ulp(gpu.read_bf16(out), oracle.add(x, y), 0, "add")
+    # 8-wide body plus a 3-element tail, in place
+    x, y = rand_bf16(rng, 5003, 4.0), rand_bf16(rng, 5003)
+    t = gpu.bf16(x)
+    gpu.run("h3_gpu_add_bf16", t, t, gpu.bf16(y), x.size)
+    assert_ulp(gpu.read_bf16(t), oracle.add(x, y), 0, "add, ragged")
 
 
 def test_euler_step(gpu):
