@@ -57,8 +57,10 @@ hk_row_vec(hk_row_args a) {
     const uint32_t row = blockIdx.x;
     const uint32_t tid = threadIdx.x;
     const size_t row_off = (size_t)row * a.width;
+    /* GATE with a null gate modulation is a plain residual add */
+    const bool gated = (MODE & HK_ROW_GATE) && a.gate_mod;
     size_t mod_base = 0;
-    if (MODE & (HK_ROW_GATE | HK_ROW_MOD))
+    if ((MODE & HK_ROW_MOD) || gated)
         mod_base = (size_t)a.row_map[row] * a.slots * a.width;
     float v[HK_ROW_CHUNKS][8];
     float local = 0.0f;
@@ -70,11 +72,17 @@ hk_row_vec(hk_row_args a) {
             if (MODE & HK_ROW_GATE) {
                 float b[8], g[8];
                 hk_unpack8(*(const uint4 *)(a.branch + row_off + col), b);
-                hk_unpack8(*(const uint4 *)(a.gate_mod + mod_base +
-                                            (size_t)a.gate_slot * a.width +
-                                            col), g);
+                if (gated) {
+                    hk_unpack8(*(const uint4 *)(a.gate_mod + mod_base +
+                                                (size_t)a.gate_slot * a.width +
+                                                col), g);
 #pragma unroll
-                for (int i = 0; i < 8; i++) v[c][i] = v[c][i] + b[i] * g[i];
+                    for (int i = 0; i < 8; i++)
+                        v[c][i] = v[c][i] + b[i] * g[i];
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) v[c][i] = v[c][i] + b[i];
+                }
                 uint4 packed = hk_pack8(v[c]);
                 *(uint4 *)(a.gated + row_off + col) = packed;
                 hk_unpack8(packed, v[c]); /* continue from the rounded row */
@@ -149,18 +157,24 @@ hk_row_scalar(hk_row_args a) {
     __shared__ float scratch[16];
     const uint32_t row = blockIdx.x;
     const size_t row_off = (size_t)row * a.width;
+    const bool gated = (MODE & HK_ROW_GATE) && a.gate_mod;
     size_t mod_base = 0;
-    if (MODE & (HK_ROW_GATE | HK_ROW_MOD))
+    if ((MODE & HK_ROW_MOD) || gated)
         mod_base = (size_t)a.row_map[row] * a.slots * a.width;
     const uint16_t *x = (MODE & HK_ROW_GATE) ? a.gated : a.input;
     float local = 0.0f;
     for (uint32_t col = threadIdx.x; col < a.width; col += blockDim.x) {
         float value = hk_bf2f(a.input[row_off + col]);
         if (MODE & HK_ROW_GATE) {
-            float g = hk_bf2f(a.gate_mod[mod_base +
-                                         (size_t)a.gate_slot * a.width + col]);
-            uint16_t rounded =
-                hk_f2bf(value + hk_bf2f(a.branch[row_off + col]) * g);
+            const float b = hk_bf2f(a.branch[row_off + col]);
+            uint16_t rounded;
+            if (gated) {
+                float g = hk_bf2f(a.gate_mod[mod_base +
+                                  (size_t)a.gate_slot * a.width + col]);
+                rounded = hk_f2bf(value + b * g);
+            } else {
+                rounded = hk_f2bf(value + b);
+            }
             a.gated[row_off + col] = rounded;
             value = hk_bf2f(rounded);
         }
@@ -1236,6 +1250,65 @@ int h3_gpu_layer_adaln_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
         hk_row_launch<base | HK_ROW_WEIGHT | HK_ROW_BIAS | HK_ROW_MOD>(gpu, a);
     }
     return hk_op_end(gpu, "layer_adaln", HK_KIND_DIRECT);
+}
+
+int h3_gpu_gate_layer_adaln_bf16(
+    h3_gpu *gpu, h3_gpu_tensor *gated_residual, h3_gpu_tensor *output,
+    const h3_gpu_tensor *residual, const h3_gpu_tensor *branch,
+    const h3_gpu_tensor *gate_modulation, const h3_gpu_tensor *norm_weight,
+    const h3_gpu_tensor *norm_bias, const h3_gpu_tensor *norm_modulation,
+    const h3_gpu_tensor *row_map, uint32_t rows, uint32_t width,
+    uint32_t slots, uint32_t gate_slot, uint32_t shift_slot,
+    uint32_t scale_slot, float epsilon) {
+    size_t count = (size_t)rows * width;
+    const bool need_map = gate_modulation || norm_modulation;
+    if ((gate_modulation && gate_slot >= slots) ||
+        (norm_modulation && (shift_slot >= slots || scale_slot >= slots)))
+        return hk_fail(gpu, "gate LayerNorm AdaLN modulation slot out of range");
+    if (!HK_REQ_BF16(residual, count, "gate LayerNorm AdaLN residual") ||
+        !HK_REQ_BF16(branch, count, "gate LayerNorm AdaLN branch") ||
+        (gate_modulation &&
+         !HK_REQ_BF16(gate_modulation, 1,
+                      "gate LayerNorm AdaLN gate modulation")) ||
+        (norm_weight && !HK_REQ_BF16(norm_weight, width, "LayerNorm weight")) ||
+        (norm_bias && !HK_REQ_BF16(norm_bias, width, "LayerNorm bias")) ||
+        (norm_modulation &&
+         !HK_REQ_BF16(norm_modulation, 1, "LayerNorm modulation")) ||
+        (need_map && !HK_REQ_U32(row_map, rows, "gate LayerNorm AdaLN row map")) ||
+        !HK_REQ_BF16(gated_residual, count,
+                     "gate LayerNorm AdaLN gated residual") ||
+        !HK_REQ_BF16(output, count, "gate LayerNorm AdaLN output") ||
+        !hk_require_active(gpu))
+        return 0;
+    hk_op_begin(gpu, "gate_layer_adaln");
+    hk_row_args a = {};
+    a.input = HK_CBF16(residual);
+    a.branch = HK_CBF16(branch);
+    a.gate_mod = gate_modulation ? HK_CBF16(gate_modulation) : NULL;
+    a.weight = norm_weight ? HK_CBF16(norm_weight) : NULL;
+    a.bias = norm_bias ? HK_CBF16(norm_bias) : NULL;
+    a.norm_mod = norm_modulation ? HK_CBF16(norm_modulation) : NULL;
+    a.row_map = need_map ? HK_CU32(row_map) : NULL;
+    a.gated = HK_BF16(gated_residual);
+    a.output = HK_BF16(output);
+    a.rows = rows; a.width = width; a.slots = slots;
+    a.gate_slot = gate_slot; a.shift_slot = shift_slot;
+    a.scale_slot = scale_slot; a.epsilon = epsilon;
+    const int base = HK_ROW_GATE | HK_ROW_NORM | HK_ROW_LAYER;
+    int key = (norm_weight ? 1 : 0) | (norm_bias ? 2 : 0) |
+              (norm_modulation ? 4 : 0);
+    switch (key) {
+    case 0: hk_row_launch<base>(gpu, a); break;
+    case 1: hk_row_launch<base | HK_ROW_WEIGHT>(gpu, a); break;
+    case 2: hk_row_launch<base | HK_ROW_BIAS>(gpu, a); break;
+    case 3: hk_row_launch<base | HK_ROW_WEIGHT | HK_ROW_BIAS>(gpu, a); break;
+    case 4: hk_row_launch<base | HK_ROW_MOD>(gpu, a); break;
+    case 5: hk_row_launch<base | HK_ROW_WEIGHT | HK_ROW_MOD>(gpu, a); break;
+    case 6: hk_row_launch<base | HK_ROW_BIAS | HK_ROW_MOD>(gpu, a); break;
+    default:
+        hk_row_launch<base | HK_ROW_WEIGHT | HK_ROW_BIAS | HK_ROW_MOD>(gpu, a);
+    }
+    return hk_op_end(gpu, "gate_layer_adaln", HK_KIND_DIRECT);
 }
 
 int h3_gpu_rms_norm_bf16(h3_gpu *gpu, h3_gpu_tensor *output,

@@ -126,6 +126,9 @@ def lib():
                                         _F]),
         "h3_gpu_layer_adaln_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _U32,
                                          _U32, _U32, _U32, _U32, _F]),
+        "h3_gpu_gate_layer_adaln_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P,
+                                              _P, _P, _P, _U32, _U32, _U32,
+                                              _U32, _U32, _U32, _F]),
         "h3_gpu_rms_norm_bf16": (_I, [_P, _P, _P, _P, _U32, _U32, _F]),
         "h3_gpu_layer_norm_bf16": (_I, [_P, _P, _P, _P, _P, _U32, _U32, _F]),
         "h3_gpu_head_rms_norm_bf16": (_I, [_P, _P, _P, _U32, _U32, _U32, _F]),

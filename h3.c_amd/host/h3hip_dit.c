@@ -462,7 +462,11 @@ static int run_h3_block(h3hip_dit *dit, uint32_t index, int fuse_next) {
 }
 
 /* One Wan-style block: self-attention, cross-attention, GELU FFN. */
-static int run_wan_block(h3hip_dit *dit, uint32_t index) {
+/* One Wan-shaped block.  Each residual update is fused with the norm that
+ * reads it (h3_gpu_gate_layer_adaln_bf16); with fuse_next the FFN gate also
+ * produces the next block's self-attention adaLN, which that block then
+ * skips. */
+static int run_wan_block(h3hip_dit *dit, uint32_t index, int fuse_next) {
     const h3hip_dit_config *c = &dit->config;
     h3_gpu *gpu = dit->gpu;
     h3hip_block *w = &dit->blocks[index];
@@ -470,11 +474,16 @@ static int run_wan_block(h3hip_dit *dit, uint32_t index) {
     const uint32_t inner = c->heads * c->head_dim;
     const float eps = c->epsilon;
     const float scale = 1.0f / sqrtf((float)c->head_dim);
-    return DIT_OP(K_ROWS, h3_gpu_layer_adaln_bf16(
-                           gpu, dit->mod_a, dit->hidden, NULL, NULL,
-                           w->modulation, dit->row_map, rows, d, SLOTS, 0, 1,
-                           eps),
-                  "self-attention adaLN") &&
+    const int adaln_ready = dit->attention_adaln_ready;
+    dit->attention_adaln_ready = 0;
+    if (!adaln_ready &&
+        !DIT_OP(K_ROWS, h3_gpu_layer_adaln_bf16(
+                            gpu, dit->mod_a, dit->hidden, NULL, NULL,
+                            w->modulation, dit->row_map, rows, d, SLOTS, 0, 1,
+                            eps),
+                "self-attention adaLN"))
+        return 0;
+    int ok =
            DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->qkv, dit->mod_a, w->qkv,
                                           w->qkv_bias, rows, d, 3 * inner),
                   "QKV projection") &&
@@ -490,15 +499,11 @@ static int run_wan_block(h3hip_dit *dit, uint32_t index) {
            DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->proj, dit->attn, w->out,
                                           w->out_bias, rows, inner, d),
                   "self-attention output") &&
-           DIT_OP(K_ROWS, h3_gpu_gate_bf16(gpu, dit->hidden, dit->hidden,
-                                        dit->proj, w->modulation,
-                                        dit->row_map, rows, d, SLOTS, 2),
-                  "self-attention gate") &&
-           DIT_OP(K_ROWS, h3_gpu_layer_adaln_bf16(
-                           gpu, dit->mod_b, dit->hidden, w->norm3,
-                           w->norm3_bias, NULL, NULL, rows, d, SLOTS, 0, 0,
-                           eps),
-                  "cross-attention norm") &&
+           DIT_OP(K_ROWS, h3_gpu_gate_layer_adaln_bf16(
+                           gpu, dit->hidden, dit->mod_b, dit->hidden,
+                           dit->proj, w->modulation, w->norm3, w->norm3_bias,
+                           NULL, dit->row_map, rows, d, SLOTS, 2, 0, 0, eps),
+                  "self-attention gate + cross-attention norm") &&
            DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->cross_q, dit->mod_b,
                                           w->cq, w->cq_bias, rows, d, inner),
                   "cross Q projection") &&
@@ -524,14 +529,11 @@ static int run_wan_block(h3hip_dit *dit, uint32_t index) {
            DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->proj, dit->cross_out,
                                           w->co, w->co_bias, rows, inner, d),
                   "cross-attention output") &&
-           DIT_OP(K_ROWS, h3_gpu_add_bf16(gpu, dit->hidden, dit->hidden,
-                                       dit->proj, rows * d),
-                  "cross-attention residual") &&
-           DIT_OP(K_ROWS, h3_gpu_layer_adaln_bf16(
-                           gpu, dit->mod_a, dit->hidden, NULL, NULL,
-                           w->modulation, dit->row_map, rows, d, SLOTS, 3, 4,
-                           eps),
-                  "FFN adaLN") &&
+           DIT_OP(K_ROWS, h3_gpu_gate_layer_adaln_bf16(
+                           gpu, dit->hidden, dit->mod_a, dit->hidden,
+                           dit->proj, NULL, NULL, NULL, w->modulation,
+                           dit->row_map, rows, d, SLOTS, 0, 3, 4, eps),
+                  "cross-attention residual + FFN adaLN") &&
            DIT_OP(K_ACT, h3_gpu_linear_gelu_bf16(gpu, dit->ffn_act,
                                                dit->mod_a, w->fc1,
                                                w->fc1_bias, rows, d, c->ffn),
@@ -539,11 +541,23 @@ static int run_wan_block(h3hip_dit *dit, uint32_t index) {
            DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->proj, dit->ffn_act,
                                           w->fc2, w->fc2_bias, rows, c->ffn,
                                           d),
-                  "FFN down") &&
-           DIT_OP(K_ROWS, h3_gpu_gate_bf16(gpu, dit->hidden, dit->hidden,
-                                        dit->proj, w->modulation,
-                                        dit->row_map, rows, d, SLOTS, 5),
-                  "FFN gate");
+                  "FFN down");
+    if (!ok) return 0;
+    if (!fuse_next)
+        return DIT_OP(K_ROWS, h3_gpu_gate_bf16(gpu, dit->hidden, dit->hidden,
+                                               dit->proj, w->modulation,
+                                               dit->row_map, rows, d, SLOTS,
+                                               5),
+                      "FFN gate");
+    if (!DIT_OP(K_ROWS, h3_gpu_gate_layer_adaln_bf16(
+                            gpu, dit->hidden, dit->mod_a, dit->hidden,
+                            dit->proj, w->modulation, NULL, NULL,
+                            dit->blocks[index + 1].modulation, dit->row_map,
+                            rows, d, SLOTS, 5, 0, 1, eps),
+                "FFN gate + next self-attention adaLN"))
+        return 0;
+    dit->attention_adaln_ready = 1;
+    return 1;
 }
 
 int h3hip_dit_run_blocks(h3hip_dit *dit, uint32_t first, uint32_t count) {
@@ -585,8 +599,9 @@ int h3hip_dit_run_blocks_ops(h3hip_dit *dit, uint32_t first, uint32_t count,
                         first + count, dit->config.blocks);
     dit->attention_adaln_ready = 0;
     for (uint32_t b = first; b < first + count; b++) {
-        int ok = is_wan(dit) ? run_wan_block(dit, b)
-                             : run_h3_block(dit, b, b + 1 < first + count);
+        const int fuse_next = b + 1 < first + count;
+        int ok = is_wan(dit) ? run_wan_block(dit, b, fuse_next)
+                             : run_h3_block(dit, b, fuse_next);
         if (!ok) return 0;
     }
     return 1;

@@ -64,8 +64,32 @@ int h3_gpu_layer_adaln_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
                             uint32_t shift_slot, uint32_t scale_slot,
                             float epsilon);
 
+/* Residual update and LayerNorm adaLN in one row pass, for pre-norm blocks
+ * whose residual update feeds the next norm:
+ *   gated_residual = bf16(residual + branch * mod[gate_slot])
+ *                    (a NULL gate_modulation gives bf16(residual + branch))
+ *   output = h3_gpu_layer_adaln_bf16 of gated_residual
+ * Bit-identical to h3_gpu_gate_bf16 (or h3_gpu_add_bf16) followed by
+ * h3_gpu_layer_adaln_bf16; gated_residual may alias residual.  No reference
+ * counterpart: the reference fuses the gate only with its RMS adaLN
+ * (h3_gpu_gate_adaln_bf16). */
+int h3_gpu_gate_layer_adaln_bf16(
+    h3_gpu *gpu, h3_gpu_tensor *gated_residual, h3_gpu_tensor *output,
+    const h3_gpu_tensor *residual, const h3_gpu_tensor *branch,
+    const h3_gpu_tensor *gate_modulation, const h3_gpu_tensor *norm_weight,
+    const h3_gpu_tensor *norm_bias, const h3_gpu_tensor *norm_modulation,
+    const h3_gpu_tensor *row_map, uint32_t rows, uint32_t width,
+    uint32_t slots, uint32_t gate_slot, uint32_t shift_slot,
+    uint32_t scale_slot, float epsilon);
+
 /* output = bf16(gelu_tanh(bf16(X . W^T + b))): GEMM with the activation in
  * its epilogue. */
+int h3_gpu_linear_gelu_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                            const h3_gpu_tensor *input,
+                            const h3_gpu_tensor *weight,
+                            const h3_gpu_tensor *bias, uint32_t rows,
+                            uint32_t input_dim, uint32_t output_dim);
+
 /* h3_gpu_patch_linear_bf16_offset / _map (h3_gpu.h:116-135) without the
  * reference's fixed checkpoint shape (5376 outputs from 32 or 96 inputs):
  * any output width and up to 4096 inputs, for reduced-width test models.
@@ -84,11 +108,6 @@ int h3_hip_patch_linear_bf16_map(h3_gpu *gpu, h3_gpu_tensor *output,
                                  const h3_gpu_tensor *row_map,
                                  uint32_t output_rows, uint32_t rows,
                                  uint32_t input_dim, uint32_t output_dim);
-int h3_gpu_linear_gelu_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
-                            const h3_gpu_tensor *input,
-                            const h3_gpu_tensor *weight,
-                            const h3_gpu_tensor *bias, uint32_t rows,
-                            uint32_t input_dim, uint32_t output_dim);
 
 /* Non-gated GELU-tanh FFN: fc2(gelu(fc1(x) + b1)) + b2.  activated is
  * caller-owned scratch of rows*hidden_dim bf16, or NULL to use the

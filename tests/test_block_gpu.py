@@ -87,6 +87,39 @@ def test_wan_block(gpu, hidden, heads, ffn, rows, text):
         dit.close()
 
 
+def test_wan_blocks_fused_across_blocks(gpu):
+    """Two Wan blocks in one call: the first block's FFN gate also produces
+    the second block's self-attention adaLN.  Against the oracle block by
+    block, and bit-identical to running the blocks in separate calls (which
+    takes the unfused gate and adaLN)."""
+    hidden, heads, ffn, rows, text = 512, 4, 1024, 200, 40
+    cfg = h3hip.dit_config(h3hip.FAMILY_WAN, hidden, heads, ffn, rows,
+                           blocks=2, text_rows=text)
+    dit = h3hip.Dit(gpu, cfg)
+    try:
+        dit.init_random(seed=19, weight_std=0.02, mod_std=0.1)
+        rng = np.random.default_rng(5)
+        cos, sin = _rope(rng, rows)
+        dit.set_rope(cos, sin)
+        ws = [{n: dit.read(n, b) for n in WAN_NAMES} for b in range(2)]
+        x0, ctx = dit.read("hidden"), dit.read("context")
+        dit.run_blocks(0, 2)
+        fused = dit.read("hidden")
+        want = x0
+        for b in range(2):
+            want = oracle.wan_block(want, ctx, ws[b],
+                                    np.zeros(rows, np.uint32),
+                                    oracle.bf16(cos), oracle.bf16(sin), rows,
+                                    text, hidden, heads, ffn)
+        _check(fused, want, "Wan 2 blocks")
+        dit.write("hidden", x0)
+        dit.run_blocks(0, 1)
+        dit.run_blocks(1, 1)
+        assert np.array_equal(dit.read("hidden"), fused)
+    finally:
+        dit.close()
+
+
 def test_h3_block_full_size_properties(gpu):
     """BASELINE config 2 shape at H3 real size (N = 2378 rows): no oracle run
     at this size; checks finiteness, determinism of a re-run and that a zero

@@ -223,6 +223,45 @@ def test_layer_adaln(gpu, width, affine, modulated):
                                  layer=True, bias=b), "LayerNorm adaLN")
 
 
+@pytest.mark.parametrize("width", [100, 5120])
+@pytest.mark.parametrize("gated", [True, False])
+@pytest.mark.parametrize("affine,modulated", [(False, True), (True, False),
+                                              (False, False), (True, True)])
+def test_gate_layer_adaln_matches_the_two_ops(gpu, width, gated, affine,
+                                              modulated):
+    """The fused residual update + LayerNorm adaLN is bit-identical to
+    h3_gpu_gate_bf16 (or h3_gpu_add_bf16) followed by h3_gpu_layer_adaln_bf16,
+    in place on the residual as the Wan block calls it; the gated residual
+    also matches the oracle's gate / add exactly."""
+    rows = 19
+    rng = np.random.default_rng(width + 4 * gated + 2 * affine + modulated)
+    res, br = rand_bf16(rng, rows * width, 2.0), rand_bf16(rng, rows * width)
+    mod, rm = _mod_setup(rng, rows, width)
+    w = gpu.bf16(rand_bf16(rng, width, 0.1, 1.0)) if affine else None
+    b = gpu.bf16(rand_bf16(rng, width, 0.1)) if affine else None
+    tmod, trm, tbr = gpu.bf16(mod), gpu.u32(rm), gpu.bf16(br)
+    # two ops
+    h1, out1 = gpu.bf16(res), gpu.new_bf16(rows * width)
+    if gated:
+        gpu.run("h3_gpu_gate_bf16", h1, h1, tbr, tmod, trm, rows, width, 6, 2)
+        want_gated = oracle.gate(res, br, mod, rm, rows, width, 6, 2)
+    else:
+        gpu.run("h3_gpu_add_bf16", h1, h1, tbr, rows * width)
+        want_gated = oracle.add(res, br)
+    gpu.run("h3_gpu_layer_adaln_bf16", out1, h1, w, b,
+            tmod if modulated else None, trm if modulated else None, rows,
+            width, 6, 3, 4, C.c_float(1e-6))
+    # fused
+    h2, out2 = gpu.bf16(res), gpu.new_bf16(rows * width)
+    gpu.run("h3_gpu_gate_layer_adaln_bf16", h2, out2, h2, tbr,
+            tmod if gated else None, w, b, tmod if modulated else None,
+            trm if (gated or modulated) else None, rows, width, 6, 2, 3, 4,
+            C.c_float(1e-6))
+    assert_ulp(gpu.read_bf16(h2), want_gated, 0, "gated residual")
+    assert np.array_equal(gpu.read_bf16(h2), gpu.read_bf16(h1))
+    assert np.array_equal(gpu.read_bf16(out2), gpu.read_bf16(out1))
+
+
 @pytest.mark.parametrize("width", [8, 5376])
 def test_rms_norm(gpu, width):
     rows = 9
