@@ -37,6 +37,7 @@
 #include "hk_internal.h"
 
 #include <math.h>
+#include <stdlib.h>
 
 #define HK_BM 256
 #define HK_BN 256
@@ -102,6 +103,9 @@ struct hk_gemm_args {
      * partial[split][pid % part_tiles][256][256] */
     float *partial;
     uint32_t split_steps, tile_base, part_tiles;
+    /* tiles [0, tile_count) of the launch, dealt to the workgroups in
+     * rounds of gridDim.x (one round when the grid covers them all) */
+    uint32_t tile_count;
 };
 
 /* Tile index -> (tile_m, tile_n): column bands of HK_GROUP_M row tiles, so
@@ -130,10 +134,14 @@ hk_gemm_mfma(hk_gemm_args g) {
                    wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = wave & 1, wn = wave >> 1;
 
-    /* ---- workgroup -> tile (XCD regroup, then GROUP_M bands) ---- */
-    uint32_t pid = blockIdx.x;
+    /* ---- workgroup -> tiles (XCD regroup, then GROUP_M bands) ----
+     * Workgroups are dealt round-robin to the 8 XCDs; the regroup gives each
+     * XCD a contiguous run of tiles in every round. */
     const uint32_t nwg = gridDim.x;
-    if ((nwg & 7u) == 0) pid = (pid & 7u) * (nwg >> 3) + (pid >> 3);
+    uint32_t slot = blockIdx.x;
+    if ((nwg & 7u) == 0) slot = (slot & 7u) * (nwg >> 3) + (slot >> 3);
+    const uint32_t tile_count = EPI == HK_EPI_PARTIAL ? nwg : g.tile_count;
+    for (uint32_t pid = slot; pid < tile_count; pid += nwg) {
     uint32_t k_first = 0, split = 0, part = 0;
     if (EPI == HK_EPI_PARTIAL) {
         split = pid / g.part_tiles;
@@ -438,6 +446,9 @@ hk_gemm_mfma(hk_gemm_args g) {
                 *(uint2 *)dst = make_uint2(v[u].x, v[u].y);
         }
     }
+    /* the next tile's loads overwrite this tile's staged rows */
+    __syncthreads();
+    } /* tiles */
 }
 
 /* Skinny GEMM for M <= 64 rows (the per-block modulation projections:
@@ -584,6 +595,21 @@ hk_splitk_reduce(hk_gemm_args g, uint32_t splits) {
         make_uint2(hk_pack2(out[0], out[1]), hk_pack2(out[2], out[3]));
 }
 
+/* Workgroups for a launch of `tiles` tiles, one workgroup per CU: the
+ * fewest that still finish in the same number of rounds, rounded up to a
+ * multiple of the 8 XCDs (480 or 1440 tiles on 256 CUs: 240 workgroups). */
+static uint32_t hk_gemm_grid(uint32_t tiles, uint32_t cus) {
+    static int persist = -1;
+    if (persist < 0) {
+        const char *e = getenv("H3_HIP_GEMM_PERSIST");
+        persist = e ? atoi(e) : 1;
+    }
+    if (!persist || tiles <= cus) return tiles;
+    const uint32_t rounds = (tiles + cus - 1) / cus;
+    const uint32_t wgs = ((tiles + rounds - 1) / rounds + 7u) & ~7u;
+    return wgs < cus ? wgs : cus;
+}
+
 int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
                  const uint16_t *bias, uint16_t *c, uint32_t m, uint32_t n,
                  uint32_t k, int epilogue) {
@@ -630,7 +656,9 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
         g.split_steps = 0;
         g.tile_base = 0;
         g.part_tiles = 0;
-        dim3 grid(g.tiles_m * g.tiles_n);
+        g.tile_count = g.tiles_m * g.tiles_n;
+        const uint32_t cus = gpu->num_cus > 0 ? (uint32_t)gpu->num_cus : 256u;
+        dim3 grid(hk_gemm_grid(g.tile_count, cus));
         /* Split-K for a sparse last round: when the tiles left after the
          * full rounds of one tile per CU (all of them, for small launches
          * like the 512-row cross-attention K/V projections) would leave over
@@ -639,7 +667,6 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
          * adds the F32 partials, the bias and the activation. */
         const uint32_t tiles = g.tiles_m * g.tiles_n;
         const uint32_t k_steps = k / HK_BK;
-        const uint32_t cus = gpu->num_cus > 0 ? (uint32_t)gpu->num_cus : 256u;
         const uint32_t full = tiles - tiles % cus, tail = tiles % cus;
         if (epilogue != HK_EPI_SWIGLU && tail && tail * 2 <= cus &&
             k_steps >= 8) {
@@ -650,12 +677,14 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
                 gpu, (size_t)splits * tail * HK_BM * HK_BN * 4);
             if (!partial) return 0;
             if (full) {
+                g.tile_count = full;
+                const dim3 fgrid(hk_gemm_grid(full, cus));
                 if (epilogue == HK_EPI_GELU)
-                    hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_GELU>, dim3(full),
+                    hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_GELU>, fgrid,
                                        dim3(HK_GEMM_THREADS), HK_GEMM_LDS,
                                        gpu->stream, g);
                 else
-                    hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_STORE>, dim3(full),
+                    hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_STORE>, fgrid,
                                        dim3(HK_GEMM_THREADS), HK_GEMM_LDS,
                                        gpu->stream, g);
             }
