@@ -4,7 +4,7 @@
         per-kernel calls / total / average / min / max duration (us)
     python h3.c_amd/rocprof_summary.py pmc <counter_collection.csv> <kernel-substring>
         per-dispatch average of every counter for the kernels matching the
-        substring, and for the calibration kernel (hk_elementwise<2>, add_bf16)
+        substring, and for the calibration kernel (hk_elementwise8<2>, add_bf16)
     python h3.c_amd/rocprof_summary.py traffic <fetch.csv> <write.csv> <kernel-substring> <calib-elements>
         HBM-side bytes per launch of the matching kernel as JSON: FETCH_SIZE
         and WRITE_SIZE (KiB per dispatch) scaled by what they read for the
@@ -35,7 +35,7 @@ def pmc(path, match):
     per = defaultdict(list)
     for r in csv.DictReader(open(path)):
         name = r["Kernel_Name"]
-        if match in name or "hk_elementwise<2>" in name:
+        if match in name or "hk_elementwise8<2>" in name:
             per[(name, r["Counter_Name"])].append(float(r["Counter_Value"]))
     for (name, counter), vals in sorted(per.items()):
         print(f"{name[:48]:48s} {counter:16s} dispatches {len(vals):4d} "
@@ -55,34 +55,29 @@ def traffic(fetch_csv, write_csv, match, calib_elements):
     import json
     calib_in = 4 * calib_elements
     calib_out = 2 * calib_elements
-    f_cal = _dispatches(fetch_csv, "hk_elementwise<2>")[-1][2] * 1024
-    w_cal = _dispatches(write_csv, "hk_elementwise<2>")[-1][2] * 1024
+    f_cal = _dispatches(fetch_csv, "hk_elementwise8<2>")[-1][2] * 1024
+    w_cal = _dispatches(write_csv, "hk_elementwise8<2>")[-1][2] * 1024
     f_scale, w_scale = calib_in / f_cal, calib_out / w_cal
     fetch = _dispatches(fetch_csv, match)
     write = _dispatches(write_csv, match)
-    per_grid = defaultdict(lambda: [0, 0.0, 0.0])
-    for (_, grid, fv), (_, _, wv) in zip(fetch, write):
-        e = per_grid[grid]
-        e[0] += 1
-        e[1] += fv * 1024 * f_scale
-        e[2] += wv * 1024 * w_scale
-    n = len(fetch)
-    total_f = sum(e[1] for e in per_grid.values())
-    total_w = sum(e[2] for e in per_grid.values())
+    per_launch = [(fv * 1024 * f_scale, wv * 1024 * w_scale)
+                  for (_, _, fv), (_, _, wv) in zip(fetch, write)]
+    n = len(per_launch)
+    total_f = sum(f for f, _ in per_launch)
+    total_w = sum(w for _, w in per_launch)
+    both = [f + w for f, w in per_launch]
     print(json.dumps({
         "kernel": match,
         "dispatches": n,
-        "calibration": {"kernel": "hk_elementwise<2> (add_bf16)",
+        "calibration": {"kernel": "hk_elementwise8<2> (add_bf16)",
                         "elements": calib_elements,
                         "fetch_scale": round(f_scale, 5),
                         "write_scale": round(w_scale, 5)},
-        "per_grid": {str(g): {"dispatches": e[0],
-                              "fetch_bytes": round(e[1] / e[0]),
-                              "write_bytes": round(e[2] / e[0])}
-                     for g, e in sorted(per_grid.items())},
         "fetch_bytes_per_launch": round(total_f / n),
         "write_bytes_per_launch": round(total_w / n),
         "bytes_per_launch": round((total_f + total_w) / n),
+        "bytes_per_launch_min": round(min(both)),
+        "bytes_per_launch_max": round(max(both)),
     }, indent=1))
 
 
