@@ -68,10 +68,14 @@ __device__ __forceinline__ uint32_t hk_swz_key(uint32_t row) {
 }
 
 /* Epilogue activations from the hardware exp2/rcp (v_exp_f32, v_rcp_f32,
- * about 1 ulp each): silu(x) = x / (1 + e^-x) and the reference's tanh-form
- * GELU with its +-10 saturation (h3_cuda_core.cu:139-158), using
- * tanh(u) = 1 - 2 / (e^(2u) + 1).  Their f32 error is far below half a
- * bf16 ulp, the rounding applied right after. */
+ * about 1 ulp each), far below half a bf16 ulp, the rounding applied right
+ * after.  silu(x) = x / (1 + e^-x).  The reference's tanh-form GELU
+ * (h3_cuda_core.cu:139-158), 0.5 x (1 + tanh u) with
+ * u = sqrt(2/pi) (x + 0.044715 x^3), is evaluated as x - x r with
+ * r = 1 / (e^(2u) + 1) and e^(2u) = 2^(x (A + B x^2)): five VALU ops and
+ * two transcendentals.  Its +-10 saturation needs no branch for finite x
+ * (u <= -10 gives 1 + e^(2u) == 1, so r == 1 and x - x r == 0; u >= 10
+ * gives |x r| below half an ulp of x); the clamps keep +-inf exact. */
 __device__ __forceinline__ float hk_exp_fast(float x) {
     return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }
@@ -81,12 +85,16 @@ __device__ __forceinline__ float hk_silu_f(float x) {
 }
 
 __device__ __forceinline__ float hk_gelu_tanh_f(float x) {
-    float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-    float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(hk_exp_fast(2.0f * inner) +
-                                                  1.0f);
-    return inner <= -10.0f ? 0.0f
-         : inner >= 10.0f  ? x
-                           : 0.5f * x * (1.0f + t);
+    /* A = 2 log2(e) sqrt(2/pi), B = 0.044715 A; v = 2 u log2(e) */
+    const float A = 2.302208198144325f, B = 0.1029432395800235f;
+    const float v = x * __builtin_fmaf(x * x, B, A);
+    const float r =
+        __builtin_amdgcn_rcpf(__builtin_amdgcn_exp2f(v) + 1.0f);
+    const float g = __builtin_fmaf(-x, r, x);
+    /* u = +-10 */
+    return v <= -28.853900817779268f ? 0.0f
+         : v >= 28.853900817779268f  ? x
+                                     : g;
 }
 
 struct hk_gemm_args {

@@ -14,7 +14,7 @@ import pytest
 
 from conftest import (adaln_terms, assert_close, assert_row_close,
                       sdpa_p_rounding_bound,
-                      assert_ulp, rand_bf16, to_f32)
+                      assert_ulp, bf16_ulp_distance, rand_bf16, to_f32)
 
 pytestmark = pytest.mark.gpu
 
@@ -95,6 +95,45 @@ def test_linear_gelu_full_round_and_split_tail(gpu):
     gpu.run("h3_gpu_linear_gelu_bf16", out, gpu.bf16(x), gpu.bf16(w),
             gpu.bf16(b), m, k, n)
     assert_close(gpu.read_bf16(out), want, what="linear+GELU", chained=1)
+
+
+@pytest.mark.parametrize("k", [64, 512])
+def test_linear_gelu_activation_exact(gpu, k):
+    """The GEMM's GELU epilogue on its own: an identity weight makes the
+    linear output exactly x, so the result must be oracle.gelu(x) over
+    -12..12, the +-10 saturation of u included.  K = 64 runs the full-tile
+    epilogue; K = 512 cuts the 16 tiles along K, so the split-K reduction
+    applies the activation.
+
+    Bound: one bf16 ulp, or an absolute |x| 2^-21.  For u below about -8.7
+    the reference's own f32 value 0.5 x (1 + tanhf(u)) is a multiple of
+    0.5 |x| 2^-24 (tanhf rounds next to -1), so there it is exact only to
+    that absolute error, and ulps of a value that small mean nothing."""
+    m, n = 4096, 64
+    rng = np.random.default_rng(k)
+    vals = oracle.bf16(np.concatenate([
+        rng.uniform(-12, 12, m * n - 8),
+        [0.0, -0.0, 1e-30, -1e-30, 5.6, -5.6, 11.0, -11.0]]).astype(
+            np.float32))
+    x = np.zeros((m, k), np.uint16)
+    x[:, :n] = vals.reshape(m, n)
+    w = np.zeros((n, k), np.uint16)
+    w[np.arange(n), np.arange(n)] = 0x3F80            # 1.0
+    out = gpu.new_bf16(m * n)
+    gpu.run("h3_gpu_linear_gelu_bf16", out, gpu.bf16(x.ravel()),
+            gpu.bf16(w.ravel()), None, m, k, n)
+    got, want = gpu.read_bf16(out), oracle.gelu(vals)
+    far = bf16_ulp_distance(got, want) > 1
+    diff = np.abs(to_f32(got) - to_f32(want))
+    limit = np.abs(to_f32(vals)) * 2.0 ** -21
+    bad = far & (diff > limit)
+    assert not bad.any(), (
+        f"{bad.sum()} GELU values off, e.g. x={to_f32(vals)[bad][:4]}"
+        f" got {to_f32(got)[bad][:4]}"
+        f" want {to_f32(want)[bad][:4]}")
+    # the absolute bound is needed only where 1 + tanhf(u) has lost bf16
+    # precision: e^(2u) < 2^-17, i.e. u < -5.9, x < -4.2
+    assert (to_f32(vals)[far] < -4.0).all(), to_f32(vals)[far].max()
 
 
 def test_ffn_gelu(gpu):
