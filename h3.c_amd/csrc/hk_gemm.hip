@@ -50,6 +50,7 @@
 #define HK_GROUP_M 8
 
 typedef int hk_v4i __attribute__((ext_vector_type(4)));
+typedef int hk_v2i __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t hk_rsrc(const void *base,
                                                           uint32_t bytes) {
@@ -135,11 +136,9 @@ __global__ void __launch_bounds__(HK_GEMM_THREADS, 1)
 __attribute__((amdgpu_waves_per_eu(1, 1)))
 hk_gemm_mfma(hk_gemm_args g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t hk_smem[];
-    const uint32_t tid = threadIdx.x;
     /* the wave index is uniform: keep it (and the LDS destinations of the
      * DMA loads derived from it) in scalar registers */
-    const uint32_t lane = tid & 63,
-                   wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t wm = wave & 1, wn = wave >> 1;
 
     /* ---- workgroup -> tiles (XCD regroup, then GROUP_M bands) ----
@@ -149,7 +148,16 @@ hk_gemm_mfma(hk_gemm_args g) {
     uint32_t slot = blockIdx.x;
     if ((nwg & 7u) == 0) slot = (slot & 7u) * (nwg >> 3) + (slot >> 3);
     const uint32_t tile_count = EPI == HK_EPI_PARTIAL ? nwg : g.tile_count;
-    for (uint32_t pid = slot; pid < tile_count; pid += nwg) {
+    for (uint32_t item = slot; item < tile_count; item += nwg) {
+    /* Everything lane-dependent is recomputed per tile: laundering the
+     * thread index keeps the compiler from hoisting those values out of the
+     * tile loop, where they would stay live through the epilogue (which
+     * needs all 256 VGPRs) and be spilled, with scratch reloads and their
+     * vmcnt waits landing in the main loop. */
+    uint32_t tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const uint32_t lane = tid & 63;
+    uint32_t pid = item;
     uint32_t k_first = 0, split = 0, part = 0;
     if (EPI == HK_EPI_PARTIAL) {
         split = pid / g.part_tiles;
@@ -375,6 +383,27 @@ hk_gemm_mfma(hk_gemm_args g) {
     constexpr uint32_t pitch = tile_cols * 2u;     /* bytes per LDS row */
     constexpr uint32_t chunks = pitch / 16u;
     const uint32_t n0 = tile_n * tile_cols;
+    /* The bias of this lane's 16 column groups, loaded once and branch-free:
+     * columns past N read as zero through the buffer bound, and without a
+     * bias every value is -0.0, which leaves any x (signed zeros included)
+     * unchanged under x + b. */
+    hk_v2i bias2[4][4];
+    if (EPI != HK_EPI_SWIGLU) {
+        const __amdgpu_buffer_rsrc_t br =
+            hk_rsrc(g.bias, g.bias ? g.n * 2u : 0u);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                if (g.bias) {
+                    bias2[i][q] = __builtin_amdgcn_raw_buffer_load_b64(
+                        br, (n0 + wn * 128u + i * 32u + q * 8u + sub) * 2u, 0,
+                        0);
+                } else {
+                    bias2[i][q] = hk_v2i{(int)0x80008000u, (int)0x80008000u};
+                }
+            }
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     auto lds_put = [&](uint32_t row, uint32_t col, uint2 v) {
@@ -399,6 +428,7 @@ hk_gemm_mfma(hk_gemm_args g) {
                     lds_put(row, wn * 64u + i * 32u + q * 8u + sub,
                             make_uint2(hk_pack2(out[0], out[1]),
                                        hk_pack2(out[2], out[3])));
+                    __builtin_amdgcn_sched_barrier(0);
                 }
         } else {
 #pragma unroll
@@ -406,16 +436,12 @@ hk_gemm_mfma(hk_gemm_args g) {
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
                     const uint32_t tcol = wn * 128u + i * 32u + q * 8u + sub;
+                    const hk_v2i b = bias2[i][q];
                     float out[4];
-#pragma unroll
-                    for (int e = 0; e < 4; e++) out[e] = acc[i][j][q * 4 + e];
-                    if (g.bias && n0 + tcol < g.n) {
-                        uint2 b = *(const uint2 *)(g.bias + n0 + tcol);
-                        out[0] += hk_bf2f(b.x & 0xffffu);
-                        out[1] += hk_bf2f(b.x >> 16);
-                        out[2] += hk_bf2f(b.y & 0xffffu);
-                        out[3] += hk_bf2f(b.y >> 16);
-                    }
+                    out[0] = acc[i][j][q * 4 + 0] + hk_bf2f(b[0] & 0xffffu);
+                    out[1] = acc[i][j][q * 4 + 1] + hk_bf2f((uint32_t)b[0] >> 16);
+                    out[2] = acc[i][j][q * 4 + 2] + hk_bf2f(b[1] & 0xffffu);
+                    out[3] = acc[i][j][q * 4 + 3] + hk_bf2f((uint32_t)b[1] >> 16);
                     if (EPI == HK_EPI_GELU) {
 #pragma unroll
                         for (int e = 0; e < 4; e++)
@@ -424,6 +450,10 @@ hk_gemm_mfma(hk_gemm_args g) {
                     lds_put(row, tcol,
                             make_uint2(hk_pack2(out[0], out[1]),
                                        hk_pack2(out[2], out[3])));
+                    /* keeps the scheduler from hoisting all 256
+                     * accumulator reads ahead of the barrier, which runs
+                     * the VGPRs out and spills */
+                    __builtin_amdgcn_sched_barrier(0);
                 }
         }
     }
