@@ -491,77 +491,94 @@ hk_gemm_mfma(hk_gemm_args g) {
 
 /* Skinny GEMM for M <= 64 rows (the per-block modulation projections:
  * time rows x 2688 against 96768 x 2688 weights).  Bound by streaming W
- * from HBM once, so no LDS: each workgroup owns a 64 (M) x 64 (N) output
- * tile, its four waves a 32 x 32 quarter, and every wave reads its MFMA
- * fragments straight from global memory (16 bytes per lane, rows past M or
- * N read as zeros through the buffer bound), one 64-wide k-step ahead of
- * the MFMAs.  X is tiny and stays in L2; each W row is read by the two
- * waves that share its column half, the second read hitting L2. */
+ * from HBM once, so no LDS and no W re-reads: each wave owns 32 W rows
+ * (output columns) and all MB x 32 rows of X, and reads its MFMA fragments
+ * straight from global memory (16 bytes per lane).  The W fragments of the
+ * next D - 1 64-wide k steps are in flight while one step's MFMAs run (the
+ * stream is latency-bound otherwise); X is small, stays in L2 and is
+ * fetched one step ahead.  The step's k offset goes in the buffer's scalar
+ * offset; rows past M or N keep a lane offset beyond the buffer and read
+ * zeros. */
+template <int MB>
 __global__ void __launch_bounds__(256)
 hk_gemm_skinny(const uint16_t *x, const uint16_t *w, const uint16_t *bias,
                uint16_t *c, uint32_t m, uint32_t n, uint32_t k,
                uint32_t x_bytes, uint32_t w_bytes) {
+    constexpr int D = 4;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t wm = wave & 1u, wn = wave >> 1;
     const uint32_t row = lane & 31u, half = lane >> 5;
-    const uint32_t m0 = blockIdx.y * 64u + wm * 32u;
-    const uint32_t n0 = blockIdx.x * 64u + wn * 32u;
+    const uint32_t n0 = (blockIdx.x * 4u + wave) * 32u;
     const __amdgpu_buffer_rsrc_t xr = hk_rsrc(x, x_bytes);
     const __amdgpu_buffer_rsrc_t wr = hk_rsrc(w, w_bytes);
-    const uint32_t xo = m0 + row < m ? ((m0 + row) * k + half * 8u) * 2u
-                                     : 0xfffffff0u;
-    const uint32_t wo = n0 + row < n ? ((n0 + row) * k + half * 8u) * 2u
-                                     : 0xfffffff0u;
-    auto load = [&](hk_v4i (&fx)[4], hk_v4i (&fw)[4], uint32_t k0) {
+    const uint32_t wo = (min(n0 + row, n) * k + half * 8u) * 2u;
+    uint32_t xo[MB];
 #pragma unroll
-        for (int s = 0; s < 4; s++) {
-            const uint32_t kb = (k0 + s * 16u) * 2u;
-            fx[s] = __builtin_amdgcn_raw_buffer_load_b128(
-                xr, xo == 0xfffffff0u ? xo : xo + kb, 0, 0);
-            fw[s] = __builtin_amdgcn_raw_buffer_load_b128(
-                wr, wo == 0xfffffff0u ? wo : wo + kb, 0, 0);
-        }
+    for (int mb = 0; mb < MB; mb++)
+        xo[mb] = (min(mb * 32u + row, m) * k + half * 8u) * 2u;
+    hk_v4i wf[D][4], xf[2][MB][4];
+    auto load_w = [&](int slot, uint32_t step) {
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            wf[slot][q] = __builtin_amdgcn_raw_buffer_load_b128(
+                wr, wo, step * 128u + q * 32u, 0);
     };
-    hk_f32x16 acc;
+    auto load_x = [&](int slot, uint32_t step) {
 #pragma unroll
-    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
-    hk_v4i fx[2][4], fw[2][4];
-    load(fx[0], fw[0], 0);
+        for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                xf[slot][mb][q] = __builtin_amdgcn_raw_buffer_load_b128(
+                    xr, xo[mb], step * 128u + q * 32u, 0);
+    };
+    hk_f32x16 acc[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[mb][r] = 0.0f;
     const uint32_t steps = k / 64u;
-    for (uint32_t s = 0; s < steps; s += 2) {
-        if (s + 1 < steps) load(fx[1], fw[1], (s + 1) * 64u);
 #pragma unroll
-        for (int q = 0; q < 4; q++)
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                __builtin_bit_cast(hk_bf16x8, fw[0][q]),
-                __builtin_bit_cast(hk_bf16x8, fx[0][q]), acc, 0, 0, 0);
-        if (s + 1 >= steps) break;
-        if (s + 2 < steps) load(fx[0], fw[0], (s + 2) * 64u);
+    for (int d = 0; d < D - 1; d++)
+        if ((uint32_t)d < steps) load_w(d, d);
+    load_x(0, 0);
+    for (uint32_t s0 = 0; s0 < steps; s0 += D) {
 #pragma unroll
-        for (int q = 0; q < 4; q++)
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                __builtin_bit_cast(hk_bf16x8, fw[1][q]),
-                __builtin_bit_cast(hk_bf16x8, fx[1][q]), acc, 0, 0, 0);
-    }
-    /* acc[r] = C[m0 + row][n0 + (r/4)*8 + half*4 + r%4] */
-    const uint32_t mm = m0 + row;
-    if (mm >= m) return;
+        for (int d = 0; d < D; d++) {
+            const uint32_t s = s0 + d;
+            if (s >= steps) break;
+            if (s + D - 1 < steps) load_w((d + D - 1) % D, s + D - 1);
+            if (s + 1 < steps) load_x((d + 1) & 1, s + 1);
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const uint32_t col = n0 + q * 8u + half * 4u;
-        if (col >= n) continue;
-        float out[4];
+            for (int q = 0; q < 4; q++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) out[e] = acc[q * 4 + e];
-        if (bias) {
-            uint2 b = *(const uint2 *)(bias + col);
-            out[0] += hk_bf2f(b.x & 0xffffu);
-            out[1] += hk_bf2f(b.x >> 16);
-            out[2] += hk_bf2f(b.y & 0xffffu);
-            out[3] += hk_bf2f(b.y >> 16);
+                for (int mb = 0; mb < MB; mb++)
+                    acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        __builtin_bit_cast(hk_bf16x8, wf[d][q]),
+                        __builtin_bit_cast(hk_bf16x8, xf[d & 1][mb][q]),
+                        acc[mb], 0, 0, 0);
         }
-        *(uint2 *)(c + (size_t)mm * n + col) =
-            uint2{hk_pack2(out[0], out[1]), hk_pack2(out[2], out[3])};
+    }
+    /* acc[mb][r] = C[mb*32 + row][n0 + (r/4)*8 + half*4 + r%4] */
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+        const uint32_t mm = mb * 32u + row;
+        if (mm >= m) continue;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint32_t col = n0 + q * 8u + half * 4u;
+            if (col >= n) continue;
+            float out[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) out[e] = acc[mb][q * 4 + e];
+            if (bias) {
+                uint2 b = *(const uint2 *)(bias + col);
+                out[0] += hk_bf2f(b.x & 0xffffu);
+                out[1] += hk_bf2f(b.x >> 16);
+                out[2] += hk_bf2f(b.y & 0xffffu);
+                out[3] += hk_bf2f(b.y >> 16);
+            }
+            *(uint2 *)(c + (size_t)mm * n + col) =
+                uint2{hk_pack2(out[0], out[1]), hk_pack2(out[2], out[3])};
+        }
     }
 }
 
@@ -654,16 +671,25 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
     if (!m || !n) return 1;
     const uint64_t w_rows = epilogue == HK_EPI_SWIGLU ? 2ull * n : n;
     const uint64_t x_bytes = (uint64_t)m * k * 2, w_bytes = w_rows * k * 2;
+    /* operand buffers must leave room for a row offset plus a k offset
+     * (2 K bytes) below 2^32: rows past the end keep such offsets, which
+     * the buffer bound turns into zeros */
+    const uint64_t margin = 2ull * k + 4096;
     const bool mfma = !gpu->reference_kernels && k % HK_BK == 0 && k > 0 &&
-                      n % 4 == 0 && x_bytes < 0xfffff000ull &&
-                      w_bytes < 0xfffff000ull &&
+                      n % 4 == 0 && x_bytes + margin < 0x100000000ull &&
+                      w_bytes + margin < 0x100000000ull &&
                       (epilogue != HK_EPI_SWIGLU || n % 64 == 0) &&
                       ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 &&
                       ((uintptr_t)c & 7) == 0 && ((uintptr_t)bias & 7) == 0;
     if (mfma && m <= 64 && epilogue == HK_EPI_STORE) {
-        hipLaunchKernelGGL(hk_gemm_skinny, dim3((n + 63) / 64, (m + 63) / 64),
-                           dim3(256), 0, gpu->stream, x, w, bias, c, m, n, k,
-                           (uint32_t)x_bytes, (uint32_t)w_bytes);
+        if (m <= 32)
+            hipLaunchKernelGGL(hk_gemm_skinny<1>, dim3((n + 127) / 128),
+                               dim3(256), 0, gpu->stream, x, w, bias, c, m, n,
+                               k, (uint32_t)x_bytes, (uint32_t)w_bytes);
+        else
+            hipLaunchKernelGGL(hk_gemm_skinny<2>, dim3((n + 127) / 128),
+                               dim3(256), 0, gpu->stream, x, w, bias, c, m, n,
+                               k, (uint32_t)x_bytes, (uint32_t)w_bytes);
         return 1;
     }
     if (mfma) {
