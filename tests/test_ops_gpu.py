@@ -41,6 +41,8 @@ def _mod_setup(rng, rows, width, slots=6, mod_rows=4):
     (1, 64, 300, True),         # skinny, one row, one K step
     (32, 384, 132, False),      # skinny, 32 rows, 6 K steps (ring of 4)
     (17, 320, 1000, True),      # skinny, 5 K steps, ragged N
+    (33, 64, 4, True),          # skinny, one row in the second half, N = 4
+    (64, 2688, 96, False),      # skinny, all 64 rows, real K, one wave of N
     (65, 192, 256, False),      # one row past the skinny limit
     (512, 5120, 5120, True),    # split-K: Wan cross K/V projection (40 tiles)
     (260, 2048, 516, True),     # split-K, ragged M and N, 4 splits
