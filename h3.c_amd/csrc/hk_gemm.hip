@@ -115,6 +115,12 @@ struct hk_gemm_args {
     /* tiles [0, tile_count) of the launch, dealt to the workgroups in
      * rounds of gridDim.x (one round when the grid covers them all) */
     uint32_t tile_count;
+    /* split-K over two problems of one shape and one X (EPI_PARTIAL):
+     * parts [pair_tiles, 2 pair_tiles) use w1 / bias1 / c1; 0 = one
+     * problem */
+    uint32_t pair_tiles;
+    const uint16_t *w1, *bias1;
+    uint16_t *c1;
 };
 
 /* Tile index -> (tile_m, tile_n): column bands of HK_GROUP_M row tiles, so
@@ -159,10 +165,13 @@ hk_gemm_mfma(hk_gemm_args g) {
     const uint32_t lane = tid & 63;
     uint32_t pid = item;
     uint32_t k_first = 0, split = 0, part = 0;
+    const uint16_t *wsrc = g.w;
     if (EPI == HK_EPI_PARTIAL) {
         split = pid / g.part_tiles;
         part = pid - split * g.part_tiles;
-        pid = g.tile_base + part;
+        const bool second = g.pair_tiles && part >= g.pair_tiles;
+        pid = g.tile_base + (second ? part - g.pair_tiles : part);
+        if (second) wsrc = g.w1;
         k_first = split * g.split_steps;
     }
     uint32_t tile_m, tile_n;
@@ -178,7 +187,7 @@ hk_gemm_mfma(hk_gemm_args g) {
      * Rows past M (and W rows past the end) get an offset beyond the
      * buffer, which the hardware returns as zeros. */
     const __amdgpu_buffer_rsrc_t xr = hk_rsrc(g.x, g.x_bytes);
-    const __amdgpu_buffer_rsrc_t wr = hk_rsrc(g.w, g.w_bytes);
+    const __amdgpu_buffer_rsrc_t wr = hk_rsrc(wsrc, g.w_bytes);
     uint32_t x_off[8], w_off[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) {
@@ -621,10 +630,14 @@ hk_splitk_reduce(hk_gemm_args g, uint32_t splits) {
     const uint32_t part = blockIdx.x >> 6;
     const uint32_t row = (blockIdx.x & 63u) * 4u + (threadIdx.x >> 6);
     const uint32_t tcol = (threadIdx.x & 63u) * 4u;
+    const bool second = g.pair_tiles && part >= g.pair_tiles;
     uint32_t tile_m, tile_n;
-    hk_tile_coords(g.tile_base + part, g.tiles_m, g.tiles_n, tile_m, tile_n);
+    hk_tile_coords(g.tile_base + (second ? part - g.pair_tiles : part),
+                   g.tiles_m, g.tiles_n, tile_m, tile_n);
     const uint32_t m = tile_m * HK_BM + row, n = tile_n * HK_BN + tcol;
     if (m >= g.m || n >= g.n) return;
+    const uint16_t *bias = second ? g.bias1 : g.bias;
+    uint16_t *c = second ? g.c1 : g.c;
     const size_t stride = (size_t)g.part_tiles * (HK_BM * HK_BN);
     const float *p = g.partial + (size_t)part * (HK_BM * HK_BN) +
                      row * HK_BN + tcol;
@@ -634,8 +647,8 @@ hk_splitk_reduce(hk_gemm_args g, uint32_t splits) {
         sum.x += v.x; sum.y += v.y; sum.z += v.z; sum.w += v.w;
     }
     float out[4] = {sum.x, sum.y, sum.z, sum.w};
-    if (g.bias) {
-        const uint2 b = *(const uint2 *)(g.bias + n);
+    if (bias) {
+        const uint2 b = *(const uint2 *)(bias + n);
         out[0] += hk_bf2f(b.x & 0xffffu);
         out[1] += hk_bf2f(b.x >> 16);
         out[2] += hk_bf2f(b.y & 0xffffu);
@@ -646,7 +659,7 @@ hk_splitk_reduce(hk_gemm_args g, uint32_t splits) {
         for (int e = 0; e < 4; e++)
             out[e] = hk_gelu_tanh_f(hk_bf2f(hk_f2bf(out[e])));
     }
-    *(uint2 *)(g.c + (size_t)m * g.n + n) =
+    *(uint2 *)(c + (size_t)m * g.n + n) =
         make_uint2(hk_pack2(out[0], out[1]), hk_pack2(out[2], out[3]));
 }
 
@@ -665,22 +678,48 @@ static uint32_t hk_gemm_grid(uint32_t tiles, uint32_t cus) {
     return wgs < cus ? wgs : cus;
 }
 
-int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
-                 const uint16_t *bias, uint16_t *c, uint32_t m, uint32_t n,
-                 uint32_t k, int epilogue) {
-    if (!m || !n) return 1;
+/* Whether the MFMA kernels take this shape and these pointers. */
+static bool hk_gemm_mfma_ok(const struct h3_gpu *gpu, const void *x,
+                            const void *w, const void *bias, const void *c,
+                            uint32_t m, uint32_t n, uint32_t k, int epilogue) {
     const uint64_t w_rows = epilogue == HK_EPI_SWIGLU ? 2ull * n : n;
     const uint64_t x_bytes = (uint64_t)m * k * 2, w_bytes = w_rows * k * 2;
     /* operand buffers must leave room for a row offset plus a k offset
      * (2 K bytes) below 2^32: rows past the end keep such offsets, which
      * the buffer bound turns into zeros */
     const uint64_t margin = 2ull * k + 4096;
-    const bool mfma = !gpu->reference_kernels && k % HK_BK == 0 && k > 0 &&
-                      n % 4 == 0 && x_bytes + margin < 0x100000000ull &&
-                      w_bytes + margin < 0x100000000ull &&
-                      (epilogue != HK_EPI_SWIGLU || n % 64 == 0) &&
-                      ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 &&
-                      ((uintptr_t)c & 7) == 0 && ((uintptr_t)bias & 7) == 0;
+    return !gpu->reference_kernels && k % HK_BK == 0 && k > 0 &&
+           n % 4 == 0 && x_bytes + margin < 0x100000000ull &&
+           w_bytes + margin < 0x100000000ull &&
+           (epilogue != HK_EPI_SWIGLU || n % 64 == 0) &&
+           ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 &&
+           ((uintptr_t)c & 7) == 0 && ((uintptr_t)bias & 7) == 0;
+}
+
+static void hk_gemm_lds_setup() {
+    if (hk_gemm_lds_ready) return;
+    (void)hipFuncSetAttribute((const void *)hk_gemm_mfma<HK_EPI_STORE>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                              HK_GEMM_LDS);
+    (void)hipFuncSetAttribute((const void *)hk_gemm_mfma<HK_EPI_SWIGLU>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                              HK_GEMM_LDS);
+    (void)hipFuncSetAttribute((const void *)hk_gemm_mfma<HK_EPI_GELU>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                              HK_GEMM_LDS);
+    (void)hipFuncSetAttribute((const void *)hk_gemm_mfma<HK_EPI_PARTIAL>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                              HK_GEMM_LDS);
+    hk_gemm_lds_ready = true;
+}
+
+int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
+                 const uint16_t *bias, uint16_t *c, uint32_t m, uint32_t n,
+                 uint32_t k, int epilogue) {
+    if (!m || !n) return 1;
+    const uint64_t w_rows = epilogue == HK_EPI_SWIGLU ? 2ull * n : n;
+    const uint64_t x_bytes = (uint64_t)m * k * 2, w_bytes = w_rows * k * 2;
+    const bool mfma = hk_gemm_mfma_ok(gpu, x, w, bias, c, m, n, k, epilogue);
     if (mfma && m <= 64 && epilogue == HK_EPI_STORE) {
         if (m <= 32)
             hipLaunchKernelGGL(hk_gemm_skinny<1>, dim3((n + 127) / 128),
@@ -693,21 +732,7 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
         return 1;
     }
     if (mfma) {
-        if (!hk_gemm_lds_ready) {
-            (void)hipFuncSetAttribute(
-                (const void *)hk_gemm_mfma<HK_EPI_STORE>,
-                hipFuncAttributeMaxDynamicSharedMemorySize, HK_GEMM_LDS);
-            (void)hipFuncSetAttribute(
-                (const void *)hk_gemm_mfma<HK_EPI_SWIGLU>,
-                hipFuncAttributeMaxDynamicSharedMemorySize, HK_GEMM_LDS);
-            (void)hipFuncSetAttribute(
-                (const void *)hk_gemm_mfma<HK_EPI_GELU>,
-                hipFuncAttributeMaxDynamicSharedMemorySize, HK_GEMM_LDS);
-            (void)hipFuncSetAttribute(
-                (const void *)hk_gemm_mfma<HK_EPI_PARTIAL>,
-                hipFuncAttributeMaxDynamicSharedMemorySize, HK_GEMM_LDS);
-            hk_gemm_lds_ready = true;
-        }
+        hk_gemm_lds_setup();
         hk_gemm_args g;
         g.x = x; g.w = w; g.bias = bias; g.c = c;
         g.m = m; g.n = n; g.k = k;
@@ -721,6 +746,9 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
         g.tile_base = 0;
         g.part_tiles = 0;
         g.tile_count = g.tiles_m * g.tiles_n;
+        g.pair_tiles = 0;
+        g.w1 = g.bias1 = NULL;
+        g.c1 = NULL;
         const uint32_t cus = gpu->num_cus > 0 ? (uint32_t)gpu->num_cus : 256u;
         dim3 grid(hk_gemm_grid(g.tile_count, cus));
         /* Split-K for a sparse last round: when the tiles left after the
@@ -800,6 +828,56 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
     return 1;
 }
 
+/* Two projections of one input with one shape, C0 = X W0^T + b0 and
+ * C1 = X W1^T + b1 (the text's cross-attention K and V).  When each alone
+ * would run entirely as split-K (together they fill at most half the CUs,
+ * as for the 512-row cross K/V projections), both go into one split-K
+ * launch and one reduction, so every CU works on both; otherwise they run
+ * one after the other. */
+int hk_gemm_bf16_pair(struct h3_gpu *gpu, const uint16_t *x,
+                      const uint16_t *w0, const uint16_t *b0, uint16_t *c0,
+                      const uint16_t *w1, const uint16_t *b1, uint16_t *c1,
+                      uint32_t m, uint32_t n, uint32_t k) {
+    if (!m || !n) return 1;
+    const uint32_t cus = gpu->num_cus > 0 ? (uint32_t)gpu->num_cus : 256u;
+    const uint32_t tiles = ((m + HK_BM - 1) / HK_BM) * ((n + HK_BN - 1) / HK_BN);
+    const uint32_t k_steps = k / HK_BK;
+    const bool paired =
+        m > 64 && k_steps >= 8 && tiles * 4 <= cus &&
+        hk_gemm_mfma_ok(gpu, x, w0, b0, c0, m, n, k, HK_EPI_STORE) &&
+        hk_gemm_mfma_ok(gpu, x, w1, b1, c1, m, n, k, HK_EPI_STORE);
+    if (!paired)
+        return hk_gemm_bf16(gpu, x, w0, b0, c0, m, n, k, HK_EPI_STORE) &&
+               hk_gemm_bf16(gpu, x, w1, b1, c1, m, n, k, HK_EPI_STORE);
+    hk_gemm_lds_setup();
+    hk_gemm_args g;
+    g.x = x; g.w = w0; g.bias = b0; g.c = c0;
+    g.m = m; g.n = n; g.k = k;
+    g.tiles_m = (m + HK_BM - 1) / HK_BM;
+    g.tiles_n = (n + HK_BN - 1) / HK_BN;
+    g.x_bytes = (uint32_t)((uint64_t)m * k * 2);
+    g.w_bytes = (uint32_t)((uint64_t)n * k * 2);
+    const uint32_t parts = 2 * tiles;
+    uint32_t splits = min(cus / parts, k_steps / 4);
+    const uint32_t steps = (k_steps + splits - 1) / splits;
+    splits = (k_steps + steps - 1) / steps;
+    float *partial = (float *)hk_splitk_space(
+        gpu, (size_t)splits * parts * HK_BM * HK_BN * 4);
+    if (!partial) return 0;
+    g.partial = partial;
+    g.split_steps = steps;
+    g.tile_base = 0;
+    g.part_tiles = parts;
+    g.tile_count = parts * splits;
+    g.pair_tiles = tiles;
+    g.w1 = w1; g.bias1 = b1; g.c1 = c1;
+    hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_PARTIAL>, dim3(parts * splits),
+                       dim3(HK_GEMM_THREADS), HK_GEMM_LDS, gpu->stream, g);
+    hipLaunchKernelGGL(hk_splitk_reduce<HK_EPI_STORE>, dim3(parts * 64),
+                       dim3(256), 0, gpu->stream, g, splits);
+    return 1;
+}
+
 /* ================================================================ ops */
 
 extern "C" {
@@ -829,6 +907,42 @@ int h3_gpu_linear_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
                       output_dim, input_dim, HK_EPI_STORE))
         return 0;
     return hk_op_end(gpu, "gemm", hk_linear_kind(rows, input_dim, output_dim));
+}
+
+int h3_hip_linear_pair_bf16(h3_gpu *gpu, h3_gpu_tensor *output0,
+                            h3_gpu_tensor *output1,
+                            const h3_gpu_tensor *input,
+                            const h3_gpu_tensor *weight0,
+                            const h3_gpu_tensor *bias0,
+                            const h3_gpu_tensor *weight1,
+                            const h3_gpu_tensor *bias1, uint32_t rows,
+                            uint32_t input_dim, uint32_t output_dim) {
+    if (!hk_require(gpu, input, (size_t)rows * input_dim, H3_GPU_BF16,
+                    "linear input") ||
+        !hk_require(gpu, weight0, (size_t)output_dim * input_dim,
+                    H3_GPU_BF16, "linear weight") ||
+        !hk_require(gpu, weight1, (size_t)output_dim * input_dim,
+                    H3_GPU_BF16, "linear weight") ||
+        !hk_require(gpu, output0, (size_t)rows * output_dim, H3_GPU_BF16,
+                    "linear output") ||
+        !hk_require(gpu, output1, (size_t)rows * output_dim, H3_GPU_BF16,
+                    "linear output") ||
+        (bias0 && !hk_require(gpu, bias0, output_dim, H3_GPU_BF16,
+                              "linear bias")) ||
+        (bias1 && !hk_require(gpu, bias1, output_dim, H3_GPU_BF16,
+                              "linear bias")) ||
+        !hk_require_active(gpu))
+        return 0;
+    if (output0 == output1)
+        return hk_fail(gpu, "paired linear outputs must be distinct");
+    hk_op_begin(gpu, "gemm_pair");
+    if (!hk_gemm_bf16_pair(gpu, HK_CBF16(input), HK_CBF16(weight0),
+                           bias0 ? HK_CBF16(bias0) : NULL, HK_BF16(output0),
+                           HK_CBF16(weight1), bias1 ? HK_CBF16(bias1) : NULL,
+                           HK_BF16(output1), rows, output_dim, input_dim))
+        return 0;
+    return hk_op_end(gpu, "gemm_pair",
+                     hk_linear_kind(rows, input_dim, output_dim));
 }
 
 int h3_gpu_linear_gelu_bf16(h3_gpu *gpu, h3_gpu_tensor *output,

@@ -138,6 +138,10 @@ enum { HK_EPI_STORE = 0, HK_EPI_SWIGLU = 1, HK_EPI_GELU = 2,
 int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *a, const uint16_t *w,
                  const uint16_t *bias, uint16_t *c, uint32_t m, uint32_t n,
                  uint32_t k, int epilogue);
+int hk_gemm_bf16_pair(struct h3_gpu *gpu, const uint16_t *x,
+                      const uint16_t *w0, const uint16_t *b0, uint16_t *c0,
+                      const uint16_t *w1, const uint16_t *b1, uint16_t *c1,
+                      uint32_t m, uint32_t n, uint32_t k);
 
 /* Flash attention; q rows [q_rows][heads][hd], k/v [kv_rows][heads][hd].
  * head_major selects [heads][q_rows][hd] output. */

@@ -124,6 +124,8 @@ def lib():
         "h3_gpu_gate_adaln_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P,
                                         _U32, _U32, _U32, _U32, _U32, _U32,
                                         _F]),
+        "h3_hip_linear_pair_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _P,
+                                         _U32, _U32, _U32]),
         "h3_gpu_layer_adaln_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _U32,
                                          _U32, _U32, _U32, _U32, _F]),
         "h3_gpu_gate_layer_adaln_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P,

@@ -511,16 +511,14 @@ static int run_wan_block(h3hip_dit *dit, uint32_t index, int fuse_next) {
                                                  w->cq_norm, rows, c->heads,
                                                  c->head_dim, eps),
                   "cross Q norm") &&
-           DIT_OP(K_CTX, h3_gpu_linear_bf16(gpu, dit->cross_k, dit->context,
-                                         w->ck, w->ck_bias, t, d, inner),
-                  "cross K projection") &&
+           DIT_OP(K_CTX, h3_hip_linear_pair_bf16(
+                          gpu, dit->cross_k, dit->cross_v, dit->context,
+                          w->ck, w->ck_bias, w->cv, w->cv_bias, t, d, inner),
+                  "cross K/V projections") &&
            DIT_OP(K_ROWS, h3_gpu_head_rms_norm_bf16(gpu, dit->cross_k,
                                                  w->ck_norm, t, c->heads,
                                                  c->head_dim, eps),
                   "cross K norm") &&
-           DIT_OP(K_CTX, h3_gpu_linear_bf16(gpu, dit->cross_v, dit->context,
-                                         w->cv, w->cv_bias, t, d, inner),
-                  "cross V projection") &&
            DIT_OP(K_ATTN, h3_gpu_sdpa_cross_bf16(gpu, dit->cross_out,
                                               dit->cross_q, dit->cross_k,
                                               dit->cross_v, rows, t, c->heads,

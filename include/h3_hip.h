@@ -82,6 +82,22 @@ int h3_gpu_gate_layer_adaln_bf16(
     uint32_t slots, uint32_t gate_slot, uint32_t shift_slot,
     uint32_t scale_slot, float epsilon);
 
+/* Two projections of one input, output0 = X . weight0^T + bias0 and
+ * output1 = X . weight1^T + bias1, each exactly as h3_gpu_linear_bf16
+ * computes it (f32 accumulation, one bf16 rounding).  Small launches
+ * (together at most half the CUs' worth of 256x256 tiles, such as the
+ * text's cross-attention K and V) share one split-K launch; others run as
+ * two linears.  Biases may be NULL.  No reference counterpart: the
+ * reference has no cross-attention. */
+int h3_hip_linear_pair_bf16(h3_gpu *gpu, h3_gpu_tensor *output0,
+                            h3_gpu_tensor *output1,
+                            const h3_gpu_tensor *input,
+                            const h3_gpu_tensor *weight0,
+                            const h3_gpu_tensor *bias0,
+                            const h3_gpu_tensor *weight1,
+                            const h3_gpu_tensor *bias1, uint32_t rows,
+                            uint32_t input_dim, uint32_t output_dim);
+
 /* output = bf16(gelu_tanh(bf16(X . W^T + b))): GEMM with the activation in
  * its epilogue. */
 int h3_gpu_linear_gelu_bf16(h3_gpu *gpu, h3_gpu_tensor *output,

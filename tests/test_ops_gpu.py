@@ -62,6 +62,34 @@ def test_linear_bf16(gpu, m, k, n, bias):
     assert_close(got, want, what=f"linear {m}x{k}x{n}")
 
 
+@pytest.mark.parametrize("m,k,n,bias", [
+    (512, 5120, 5120, True),    # the Wan cross K/V shape: one paired launch
+    (77, 512, 640, False),      # 3 + 3 tiles, 8 K steps, ragged M and N
+    (600, 1088, 256, True),     # ragged M, a short last split
+    (4096, 512, 4352, True),    # too many tiles to pair: two linears
+])
+def test_linear_pair(gpu, m, k, n, bias):
+    """h3_hip_linear_pair_bf16: each output as h3_gpu_linear_bf16 would give
+    it, against the oracle, whether the two share one split-K launch or
+    not."""
+    rng = np.random.default_rng(m + 3 * k + n)
+    x = rand_bf16(rng, m * k)
+    w0, w1 = rand_bf16(rng, n * k, 0.05), rand_bf16(rng, n * k, 0.05)
+    b0 = rand_bf16(rng, n, 0.1) if bias else None
+    b1 = rand_bf16(rng, n, 0.1) if bias else None
+    o0, o1 = gpu.new_bf16(m * n), gpu.new_bf16(m * n)
+    gpu.run("h3_hip_linear_pair_bf16", o0, o1, gpu.bf16(x), gpu.bf16(w0),
+            gpu.bf16(b0) if bias else None, gpu.bf16(w1),
+            gpu.bf16(b1) if bias else None, m, k, n)
+    assert_close(gpu.read_bf16(o0), oracle.linear(x, w0, b0, m, k, n),
+                 what=f"pair[0] {m}x{k}x{n}")
+    assert_close(gpu.read_bf16(o1), oracle.linear(x, w1, b1, m, k, n),
+                 what=f"pair[1] {m}x{k}x{n}")
+    with pytest.raises(RuntimeError, match="distinct"):
+        gpu.run("h3_hip_linear_pair_bf16", o0, o0, gpu.bf16(x), gpu.bf16(w0),
+                None, gpu.bf16(w1), None, m, k, n)
+
+
 def test_linear_stats_kind(gpu):
     """Routing-shape rule of the stats counters (reference
     h3_cuda_core.cu:838-841): rows >= 32, in >= 256, out >= 256 -> kind 1."""
