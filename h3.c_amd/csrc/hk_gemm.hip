@@ -142,6 +142,10 @@ __global__ void __launch_bounds__(HK_GEMM_THREADS, 1)
 __attribute__((amdgpu_waves_per_eu(1, 1)))
 hk_gemm_mfma(hk_gemm_args g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t hk_smem[];
+    constexpr bool partial =
+        EPI == HK_EPI_PARTIAL || EPI == HK_EPI_PARTIAL_SWIGLU;
+    constexpr bool swiglu_rows =
+        EPI == HK_EPI_SWIGLU || EPI == HK_EPI_PARTIAL_SWIGLU;
     /* the wave index is uniform: keep it (and the LDS destinations of the
      * DMA loads derived from it) in scalar registers */
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -153,7 +157,7 @@ hk_gemm_mfma(hk_gemm_args g) {
     const uint32_t nwg = gridDim.x;
     uint32_t slot = blockIdx.x;
     if ((nwg & 7u) == 0) slot = (slot & 7u) * (nwg >> 3) + (slot >> 3);
-    const uint32_t tile_count = EPI == HK_EPI_PARTIAL ? nwg : g.tile_count;
+    const uint32_t tile_count = partial ? nwg : g.tile_count;
     for (uint32_t item = slot; item < tile_count; item += nwg) {
     /* Everything lane-dependent is recomputed per tile: laundering the
      * thread index keeps the compiler from hoisting those values out of the
@@ -166,7 +170,7 @@ hk_gemm_mfma(hk_gemm_args g) {
     uint32_t pid = item;
     uint32_t k_first = 0, split = 0, part = 0;
     const uint16_t *wsrc = g.w;
-    if (EPI == HK_EPI_PARTIAL) {
+    if (partial) {
         split = pid / g.part_tiles;
         part = pid - split * g.part_tiles;
         const bool second = g.pair_tiles && part >= g.pair_tiles;
@@ -197,7 +201,7 @@ hk_gemm_mfma(hk_gemm_args g) {
         const uint32_t xm = min(m0 + row, g.m);
         x_off[j] = xm * g.k * 2u + chunk * 16u + k_first * (HK_BK * 2u);
         uint32_t wrow;
-        if (EPI == HK_EPI_SWIGLU) {
+        if (swiglu_rows) {
             /* W tile rows: per wave half 64 gate rows then 64 up rows */
             const uint32_t half = row >> 7, within = row & 127u;
             const uint32_t col = tile_n * 128u + half * 64u + (within & 63u);
@@ -253,7 +257,7 @@ hk_gemm_mfma(hk_gemm_args g) {
      * wave stalls issue).  Every load still has over two substeps to land
      * before the barrier that waits for it. */
     const uint32_t k_steps =
-        EPI == HK_EPI_PARTIAL ? min(g.split_steps, g.k / HK_BK - k_first)
+        partial ? min(g.split_steps, g.k / HK_BK - k_first)
                               : g.k / HK_BK;
     const uint32_t frag_row = lane & 31u;
     const uint32_t frag_half = lane >> 5;
@@ -370,7 +374,7 @@ hk_gemm_mfma(hk_gemm_args g) {
      * chunk c ^ (r % chunks), so both the 8-byte fragment writes (32 rows,
      * one column group) and the row reads spread over the banks. */
     const uint32_t sub = frag_half * 4u;
-    if (EPI == HK_EPI_PARTIAL) {
+    if (partial) {
         /* tile-local F32, whole tile (rows and columns past the matrix are
          * zeros that the reduction skips) */
         float *ptile = g.partial +
@@ -627,6 +631,39 @@ static bool hk_gemm_lds_ready = false;
 template <int EPI>
 __global__ void __launch_bounds__(256)
 hk_splitk_reduce(hk_gemm_args g, uint32_t splits) {
+    if (EPI == HK_EPI_SWIGLU) {
+        /* 8 tile rows per workgroup, 4 output columns per thread: output
+         * column c of the tile (128 per tile) is W-tile row (c/64)*128 +
+         * c%64 (gate) and that + 64 (up); out = bf16(silu(bf16 g) bf16 u) */
+        const uint32_t part = blockIdx.x >> 5;
+        const uint32_t row = (blockIdx.x & 31u) * 8u + (threadIdx.x >> 5);
+        const uint32_t c4 = (threadIdx.x & 31u) * 4u;
+        uint32_t tile_m, tile_n;
+        hk_tile_coords(g.tile_base + part, g.tiles_m, g.tiles_n, tile_m,
+                       tile_n);
+        const uint32_t m = tile_m * HK_BM + row, n = tile_n * 128u + c4;
+        if (m >= g.m || n >= g.n) return;
+        const size_t stride = (size_t)g.part_tiles * (HK_BM * HK_BN);
+        const float *p = g.partial + (size_t)part * (HK_BM * HK_BN) +
+                         row * HK_BN + (c4 >> 6) * 128u + (c4 & 63u);
+        float4 gs = *(const float4 *)p, us = *(const float4 *)(p + 64);
+        for (uint32_t s = 1; s < splits; s++) {
+            const float4 gv = *(const float4 *)(p + s * stride);
+            const float4 uv = *(const float4 *)(p + s * stride + 64);
+            gs.x += gv.x; gs.y += gv.y; gs.z += gv.z; gs.w += gv.w;
+            us.x += uv.x; us.y += uv.y; us.z += uv.z; us.w += uv.w;
+        }
+        const float gg[4] = {gs.x, gs.y, gs.z, gs.w};
+        const float uu[4] = {us.x, us.y, us.z, us.w};
+        float out[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            out[e] = hk_silu_f(hk_bf2f(hk_f2bf(gg[e]))) *
+                     hk_bf2f(hk_f2bf(uu[e]));
+        *(uint2 *)(g.c + (size_t)m * g.n + n) =
+            make_uint2(hk_pack2(out[0], out[1]), hk_pack2(out[2], out[3]));
+        return;
+    }
     const uint32_t part = blockIdx.x >> 6;
     const uint32_t row = (blockIdx.x & 63u) * 4u + (threadIdx.x >> 6);
     const uint32_t tcol = (threadIdx.x & 63u) * 4u;
@@ -710,6 +747,9 @@ static void hk_gemm_lds_setup() {
     (void)hipFuncSetAttribute((const void *)hk_gemm_mfma<HK_EPI_PARTIAL>,
                               hipFuncAttributeMaxDynamicSharedMemorySize,
                               HK_GEMM_LDS);
+    (void)hipFuncSetAttribute(
+        (const void *)hk_gemm_mfma<HK_EPI_PARTIAL_SWIGLU>,
+        hipFuncAttributeMaxDynamicSharedMemorySize, HK_GEMM_LDS);
     hk_gemm_lds_ready = true;
 }
 
@@ -756,12 +796,13 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
          * like the 512-row cross-attention K/V projections) would leave over
          * half the CUs idle, those tiles are cut along K into up to
          * num_cus / tiles pieces of at least 4 K steps each; a reduction
-         * adds the F32 partials, the bias and the activation. */
+         * adds the F32 partials, the bias and the activation (SwiGLU: the
+         * gate and up sums, each rounded to bf16 as the fused epilogue
+         * does). */
         const uint32_t tiles = g.tiles_m * g.tiles_n;
         const uint32_t k_steps = k / HK_BK;
         const uint32_t full = tiles - tiles % cus, tail = tiles % cus;
-        if (epilogue != HK_EPI_SWIGLU && tail && tail * 2 <= cus &&
-            k_steps >= 8) {
+        if (tail && tail * 2 <= cus && k_steps >= 8) {
             uint32_t splits = min(cus / tail, k_steps / 4);
             const uint32_t steps = (k_steps + splits - 1) / splits;
             splits = (k_steps + steps - 1) / steps;
@@ -775,6 +816,10 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
                     hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_GELU>, fgrid,
                                        dim3(HK_GEMM_THREADS), HK_GEMM_LDS,
                                        gpu->stream, g);
+                else if (epilogue == HK_EPI_SWIGLU)
+                    hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_SWIGLU>, fgrid,
+                                       dim3(HK_GEMM_THREADS), HK_GEMM_LDS,
+                                       gpu->stream, g);
                 else
                     hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_STORE>, fgrid,
                                        dim3(HK_GEMM_THREADS), HK_GEMM_LDS,
@@ -784,10 +829,19 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
             g.split_steps = steps;
             g.tile_base = full;
             g.part_tiles = tail;
-            hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_PARTIAL>,
-                               dim3(tail * splits), dim3(HK_GEMM_THREADS),
-                               HK_GEMM_LDS, gpu->stream, g);
-            if (epilogue == HK_EPI_GELU)
+            if (epilogue == HK_EPI_SWIGLU)
+                hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_PARTIAL_SWIGLU>,
+                                   dim3(tail * splits), dim3(HK_GEMM_THREADS),
+                                   HK_GEMM_LDS, gpu->stream, g);
+            else
+                hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_PARTIAL>,
+                                   dim3(tail * splits), dim3(HK_GEMM_THREADS),
+                                   HK_GEMM_LDS, gpu->stream, g);
+            if (epilogue == HK_EPI_SWIGLU)
+                hipLaunchKernelGGL(hk_splitk_reduce<HK_EPI_SWIGLU>,
+                                   dim3(tail * 32), dim3(256), 0, gpu->stream,
+                                   g, splits);
+            else if (epilogue == HK_EPI_GELU)
                 hipLaunchKernelGGL(hk_splitk_reduce<HK_EPI_GELU>,
                                    dim3(tail * 64), dim3(256), 0, gpu->stream,
                                    g, splits);

@@ -130,7 +130,8 @@ double hk_now(void);
 
 /* GEMM epilogues */
 enum { HK_EPI_STORE = 0, HK_EPI_SWIGLU = 1, HK_EPI_GELU = 2,
-       HK_EPI_PARTIAL = 3 /* internal: f32 split-K partial tiles */ };
+       HK_EPI_PARTIAL = 3, /* internal: f32 split-K partial tiles */
+       HK_EPI_PARTIAL_SWIGLU = 4 /* internal: the same, SwiGLU W rows */ };
 
 /* C[M,N] = epi(A[M,K] . W[N,K]^T + bias).  For HK_EPI_SWIGLU the weight has
  * 2*N rows (gate rows [0,N), up rows [N,2N)) and C is the [M,N] activation.

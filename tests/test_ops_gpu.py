@@ -101,8 +101,13 @@ def test_linear_stats_kind(gpu):
     assert gpu.stats().mps_linear_dispatches == before + 1
 
 
-@pytest.mark.parametrize("rows,d,ffn", [(64, 256, 512), (300, 1024, 1536),
-                                        (130, 5376, 512)])
+@pytest.mark.parametrize("rows,d,ffn", [
+    (64, 256, 512),       # 4 SwiGLU tiles, too few K steps to split
+    (300, 1024, 1536),    # 24 tiles, cut along K (SwiGLU split-K reduce)
+    (130, 5376, 512),     # 4 tiles at the real hidden size, 21 splits
+    (300, 512, 4608),     # 72 tiles, 2 splits
+    (300, 512, 17408),    # 272 tiles: one full round + a 16-tile split tail
+])
 def test_mlp_swiglu(gpu, rows, d, ffn):
     rng = np.random.default_rng(rows + d + ffn)
     x = rand_bf16(rng, rows * d)
