@@ -84,7 +84,7 @@ KERNEL_NAMES = {
                   "down)",
     "gemm_gelu": "hk_gemm_mfma<2> + split tail (FFN up + GELU)",
     "context_kv": "split-K hk_gemm_mfma<3> + reduce (cross K/V of the text)",
-    "attention": "hk_flash_fwd<false> (self + cross)",
+    "attention": "hk_flash_fwd<false, false> (self + cross)",
     "row_ops": "adaLN / gates / Q-K norm + RoPE / head norm / residual rows",
 }
 

@@ -85,9 +85,14 @@ struct hk_attn_args {
      * (lists sorted), or null for dense */
     const uint32_t *sparse_ptr, *sparse_idx;
     uint32_t sparse_blocks; /* query blocks in the CSR */
+    /* split launch (SPLIT): work item full_units + pid / pieces, key tiles
+     * of piece pid % pieces; unnormalised f32 O into part_o[pid][256][128],
+     * (running max in the exp2 domain, sum) into part_ml[pid][256] */
+    uint32_t full_units, pieces;
+    float *part_o, *part_ml;
 };
 
-template <bool SPARSE>
+template <bool SPARSE, bool SPLIT>
 __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t hk_lds[];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
@@ -96,7 +101,8 @@ __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
     uint32_t pid = blockIdx.x;
     const uint32_t nwg = gridDim.x;
     if ((nwg & 7u) == 0) pid = (pid & 7u) * (nwg >> 3) + (pid >> 3);
-    const uint32_t qblock = pid % a.q_blocks, head = pid / a.q_blocks;
+    const uint32_t item = SPLIT ? a.full_units + pid / a.pieces : pid;
+    const uint32_t qblock = item % a.q_blocks, head = item / a.q_blocks;
     const uint32_t row_stride = a.heads * HK_HD; /* elements */
 
     const __amdgpu_buffer_rsrc_t qr = hk_attn_rsrc(a.q, a.q_bytes);
@@ -189,8 +195,14 @@ __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
      * and waves 0-3 (first block) / 4-7 (second block) run the MFMAs and
      * softmax only on tiles of their own block's list.  A list's length is
      * clamped to the dense tile count, as in the reference kernel. */
-    const uint32_t dense = (a.kv_rows + HK_KT - 1) / HK_KT;
-    uint32_t dense_next = 0, ia = 0, ea = 0, ib = 0, eb = 0;
+    const uint32_t all_tiles = (a.kv_rows + HK_KT - 1) / HK_KT;
+    /* a split piece covers key tiles [first_tile, dense) */
+    const uint32_t piece_tiles =
+        SPLIT ? (all_tiles + a.pieces - 1) / a.pieces : all_tiles;
+    const uint32_t first_tile = SPLIT ? (pid % a.pieces) * piece_tiles : 0;
+    const uint32_t dense =
+        SPLIT ? min(all_tiles, first_tile + piece_tiles) : all_tiles;
+    uint32_t dense_next = first_tile, ia = 0, ea = 0, ib = 0, eb = 0;
     if (SPARSE) {
         const uint32_t qa = qblock * 2u, qb = qa + 1u;
         ia = a.sparse_ptr[qa];
@@ -347,10 +359,10 @@ __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
     /* the key-range mask is compiled only into the step of the last dense
      * tile, the only tile with keys past kv_rows */
     if constexpr (!SPARSE) {
-        for (uint32_t t = 0; t + 1 < dense; t++)
-            tile_step(t, t, t + 1, true, true,
+        for (uint32_t t = first_tile; t + 1 < dense; t++)
+            tile_step(t - first_tile, t, t + 1, true, true,
                       std::integral_constant<bool, false>());
-        tile_step(dense - 1, dense - 1, 0, false, true,
+        tile_step(dense - 1 - first_tile, dense - 1, 0, false, true,
                   std::integral_constant<bool, true>());
     } else {
         for (uint32_t t = 0; have; t++) {
@@ -367,6 +379,26 @@ __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
         }
     }
 
+    if constexpr (SPLIT) {
+        /* unnormalised partials for the combine kernel */
+#pragma unroll
+        for (int g = 0; g < HK_QG; g++) {
+            const uint32_t ql = wave * (32u * HK_QG) + g * 32u + col;
+            float *po = a.part_o + ((size_t)pid * HK_QB + ql) * HK_HD;
+#pragma unroll
+            for (int d = 0; d < 4; d++)
+#pragma unroll
+                for (int blk = 0; blk < 4; blk++)
+                    *(float4 *)(po + d * 32u + blk * 8u + half * 4u) =
+                        make_float4(o[d][g][blk * 4 + 0], o[d][g][blk * 4 + 1],
+                                    o[d][g][blk * 4 + 2], o[d][g][blk * 4 + 3]);
+            const float l = l_part[g] + __shfl_xor(l_part[g], 32, 64);
+            if (half == 0)
+                *(float2 *)(a.part_ml + ((size_t)pid * HK_QB + ql) * 2u) =
+                    make_float2(m_run[g], l);
+        }
+        return;
+    }
     /* ---- normalise and store: lane owns query column `col` of group g and
      * dims d*32 + (r/4)*8 + 4*half + r%4 */
 #pragma unroll
@@ -441,7 +473,46 @@ hk_attn_reference(const uint16_t *q, const uint16_t *k, const uint16_t *v,
     }
 }
 
+/* Combines the key-range pieces of the split work items: per query, with
+ * the pieces' running maxima m_p (exp2 domain), sums l_p and unnormalised
+ * O_p, O = sum_p 2^(m_p - M) O_p / sum_p 2^(m_p - M) l_p, M = max_p m_p.
+ * 8 queries per workgroup, 4 dims per thread. */
+__global__ void __launch_bounds__(256) hk_flash_combine(hk_attn_args a) {
+    const uint32_t titem = blockIdx.x >> 5;
+    const uint32_t ql = (blockIdx.x & 31u) * 8u + (threadIdx.x >> 5);
+    const uint32_t d4 = (threadIdx.x & 31u) * 4u;
+    const uint32_t item = a.full_units + titem;
+    const uint32_t qblock = item % a.q_blocks, head = item / a.q_blocks;
+    const uint32_t q = qblock * HK_QB + ql;
+    if (q >= a.q_rows) return;
+    const size_t first = (size_t)titem * a.pieces;
+    float top = -INFINITY;
+    for (uint32_t p = 0; p < a.pieces; p++)
+        top = fmaxf(top, a.part_ml[((first + p) * HK_QB + ql) * 2u]);
+    float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float l = 0.0f;
+    for (uint32_t p = 0; p < a.pieces; p++) {
+        const float2 ml =
+            *(const float2 *)(a.part_ml + ((first + p) * HK_QB + ql) * 2u);
+        const float w = __builtin_amdgcn_exp2f(ml.x - top);
+        const float4 op = *(const float4 *)(a.part_o +
+                                            ((first + p) * HK_QB + ql) * HK_HD +
+                                            d4);
+        sum.x += w * op.x; sum.y += w * op.y;
+        sum.z += w * op.z; sum.w += w * op.w;
+        l += w * ml.y;
+    }
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    uint16_t *out = a.head_major
+        ? a.o + ((size_t)head * a.q_rows + q) * HK_HD
+        : a.o + (size_t)q * a.heads * HK_HD + (size_t)head * HK_HD;
+    *(uint2 *)(out + d4) = make_uint2(hk_pack2(sum.x * inv, sum.y * inv),
+                                      hk_pack2(sum.z * inv, sum.w * inv));
+}
+
 static bool hk_attn_lds_ready = false;
+/* the comma in a template argument list confuses hipLaunchKernelGGL */
+#define HK_FLASH(sparse, split) (hk_flash_fwd<sparse, split>)
 
 int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
                       const uint16_t *k, const uint16_t *v, uint16_t *o,
@@ -465,12 +536,15 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
                        ((uintptr_t)v & 15) == 0 && ((uintptr_t)o & 7) == 0;
     if (flash) {
         if (!hk_attn_lds_ready) {
-            (void)hipFuncSetAttribute((const void *)hk_flash_fwd<false>,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      HK_ATTN_LDS);
-            (void)hipFuncSetAttribute((const void *)hk_flash_fwd<true>,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      HK_ATTN_LDS);
+            (void)hipFuncSetAttribute(
+                (const void *)hk_flash_fwd<false, false>,
+                hipFuncAttributeMaxDynamicSharedMemorySize, HK_ATTN_LDS);
+            (void)hipFuncSetAttribute(
+                (const void *)hk_flash_fwd<true, false>,
+                hipFuncAttributeMaxDynamicSharedMemorySize, HK_ATTN_LDS);
+            (void)hipFuncSetAttribute(
+                (const void *)hk_flash_fwd<false, true>,
+                hipFuncAttributeMaxDynamicSharedMemorySize, HK_ATTN_LDS);
             hk_attn_lds_ready = true;
         }
         hk_attn_args a;
@@ -486,14 +560,55 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
         a.sparse_ptr = masked ? gpu->sparse_ptr : NULL;
         a.sparse_idx = masked ? gpu->sparse_idx : NULL;
         a.sparse_blocks = (q_rows + 127u) / 128u;
-        if (masked)
-            hipLaunchKernelGGL(hk_flash_fwd<true>,
-                               dim3(a.q_blocks * heads), dim3(HK_THREADS),
-                               HK_ATTN_LDS, gpu->stream, a);
-        else
-            hipLaunchKernelGGL(hk_flash_fwd<false>,
-                               dim3(a.q_blocks * heads), dim3(HK_THREADS),
-                               HK_ATTN_LDS, gpu->stream, a);
+        const uint32_t units = a.q_blocks * heads;
+        a.full_units = units;
+        a.pieces = 1;
+        a.part_o = a.part_ml = NULL;
+        if (masked) {
+            hipLaunchKernelGGL(HK_FLASH(true, false), dim3(units),
+                               dim3(HK_THREADS), HK_ATTN_LDS, gpu->stream, a);
+            return 1;
+        }
+        /* With one workgroup per CU the items run in rounds of num_cus.  A
+         * sparse last round (the H3 block at 2378 rows: 560 items = 2
+         * rounds + 48) is cut along the keys into pieces that fill the
+         * CUs, when that takes at most 0.6 of a round instead of one; a
+         * combine kernel merges the pieces' partial softmax. */
+        const uint32_t cus = gpu->num_cus > 0 ? (uint32_t)gpu->num_cus : 256u;
+        const uint32_t kv_tiles = (kv_rows + HK_KT - 1) / HK_KT;
+        const uint32_t tail = units % cus;
+        uint32_t pieces = 1;
+        float best = 1.0f;
+        for (uint32_t s = 2; tail && s <= 8 && kv_tiles >= 2 * s; s++) {
+            const float cost = (float)((tail * s + cus - 1) / cus) / (float)s;
+            if (cost < best - 1e-6f) {
+                best = cost;
+                pieces = s;
+            }
+        }
+        if (best > 0.6f) pieces = 1;
+        if (pieces > 1) {
+            /* every piece non-empty */
+            const uint32_t per = (kv_tiles + pieces - 1) / pieces;
+            pieces = (kv_tiles + per - 1) / per;
+            const size_t parts = (size_t)tail * pieces;
+            float *buf = (float *)hk_splitk_space(
+                gpu, parts * HK_QB * (HK_HD + 2) * sizeof(float));
+            if (!buf) return 0;
+            a.part_o = buf;
+            a.part_ml = buf + parts * HK_QB * HK_HD;
+            a.full_units = units - tail;
+            a.pieces = pieces;
+        }
+        if (a.full_units)
+            hipLaunchKernelGGL(HK_FLASH(false, false), dim3(a.full_units),
+                               dim3(HK_THREADS), HK_ATTN_LDS, gpu->stream, a);
+        if (pieces > 1) {
+            hipLaunchKernelGGL(HK_FLASH(false, true), dim3(tail * pieces),
+                               dim3(HK_THREADS), HK_ATTN_LDS, gpu->stream, a);
+            hipLaunchKernelGGL(hk_flash_combine, dim3(tail * 32), dim3(256),
+                               0, gpu->stream, a);
+        }
         return 1;
     }
     if ((size_t)kv_rows * sizeof(float) > 64 * 1024)

@@ -393,9 +393,10 @@ def test_qkv_rope(gpu, grouped, hd, rope_half):
 
 @pytest.mark.parametrize("q_rows,kv_rows,heads", [
     (100, 100, 2),      # reference test_cuda_attention.c hd128 N=100
-    (300, 300, 3),      # two 256-query blocks, ragged key tail
+    (300, 300, 3),      # two 256-query blocks, ragged key tail, 2 pieces
     (64, 64, 1),        # exactly one key tile
-    (1000, 1000, 2),
+    (1000, 1000, 2),    # 8 work items on 256 CUs: 8 key-range pieces each
+    (2378, 2378, 4),    # H3 length: 40 items, 8 pieces of 5 key tiles
     (300, 77, 2),       # cross attention, short context
     (70, 513, 2),       # cross attention, more keys than queries
 ])
@@ -419,9 +420,10 @@ def test_sdpa(gpu, q_rows, kv_rows, heads):
                                                  heads, hd, scale))
 
 
-def test_sdpa_head_major(gpu):
-    n, heads, hd = 150, 2, 128
-    rng = np.random.default_rng(21)
+@pytest.mark.parametrize("n", [150, 1000])   # 1000: key-split pieces
+def test_sdpa_head_major(gpu, n):
+    heads, hd = 2, 128
+    rng = np.random.default_rng(21 + n)
     q, k, v = (rand_bf16(rng, n * heads * hd) for _ in range(3))
     scale = 1.0 / math.sqrt(hd)
     want = oracle.sdpa(q, k, v, n, n, heads, hd, scale, head_major=True)
