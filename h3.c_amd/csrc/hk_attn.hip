@@ -206,10 +206,22 @@ __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
     if (SPARSE) {
         const uint32_t qa = qblock * 2u, qb = qa + 1u;
         ia = a.sparse_ptr[qa];
-        ea = min(a.sparse_ptr[qa + 1], ia + dense);
+        ea = min(a.sparse_ptr[qa + 1], ia + all_tiles);
         if (qb < a.sparse_blocks) {
             ib = a.sparse_ptr[qb];
-            eb = min(a.sparse_ptr[qb + 1], ib + dense);
+            eb = min(a.sparse_ptr[qb + 1], ib + all_tiles);
+        }
+        if (SPLIT) {
+            /* this piece's key tiles [first_tile, dense) of the sorted
+             * lists */
+            while (ia < ea && a.sparse_idx[ia] < first_tile) ia++;
+            uint32_t e = ia;
+            while (e < ea && a.sparse_idx[e] < dense) e++;
+            ea = e;
+            while (ib < eb && a.sparse_idx[ib] < first_tile) ib++;
+            e = ib;
+            while (e < eb && a.sparse_idx[e] < dense) e++;
+            eb = e;
         }
     }
     const bool first_block = wave < HK_WAVES / 2;
@@ -494,7 +506,9 @@ __global__ void __launch_bounds__(256) hk_flash_combine(hk_attn_args a) {
     for (uint32_t p = 0; p < a.pieces; p++) {
         const float2 ml =
             *(const float2 *)(a.part_ml + ((first + p) * HK_QB + ql) * 2u);
-        const float w = __builtin_amdgcn_exp2f(ml.x - top);
+        /* a sparse piece may hold no key tile of this query block */
+        const float w =
+            ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - top);
         const float4 op = *(const float4 *)(a.part_o +
                                             ((first + p) * HK_QB + ql) * HK_HD +
                                             d4);
@@ -545,6 +559,9 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
             (void)hipFuncSetAttribute(
                 (const void *)hk_flash_fwd<false, true>,
                 hipFuncAttributeMaxDynamicSharedMemorySize, HK_ATTN_LDS);
+            (void)hipFuncSetAttribute(
+                (const void *)hk_flash_fwd<true, true>,
+                hipFuncAttributeMaxDynamicSharedMemorySize, HK_ATTN_LDS);
             hk_attn_lds_ready = true;
         }
         hk_attn_args a;
@@ -564,11 +581,6 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
         a.full_units = units;
         a.pieces = 1;
         a.part_o = a.part_ml = NULL;
-        if (masked) {
-            hipLaunchKernelGGL(HK_FLASH(true, false), dim3(units),
-                               dim3(HK_THREADS), HK_ATTN_LDS, gpu->stream, a);
-            return 1;
-        }
         /* With one workgroup per CU the items run in rounds of num_cus.  A
          * sparse last round (the H3 block at 2378 rows: 560 items = 2
          * rounds + 48) is cut along the keys into pieces that fill the
@@ -600,12 +612,25 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
             a.full_units = units - tail;
             a.pieces = pieces;
         }
-        if (a.full_units)
-            hipLaunchKernelGGL(HK_FLASH(false, false), dim3(a.full_units),
-                               dim3(HK_THREADS), HK_ATTN_LDS, gpu->stream, a);
+        if (a.full_units) {
+            if (masked)
+                hipLaunchKernelGGL(HK_FLASH(true, false), dim3(a.full_units),
+                                   dim3(HK_THREADS), HK_ATTN_LDS, gpu->stream,
+                                   a);
+            else
+                hipLaunchKernelGGL(HK_FLASH(false, false), dim3(a.full_units),
+                                   dim3(HK_THREADS), HK_ATTN_LDS, gpu->stream,
+                                   a);
+        }
         if (pieces > 1) {
-            hipLaunchKernelGGL(HK_FLASH(false, true), dim3(tail * pieces),
-                               dim3(HK_THREADS), HK_ATTN_LDS, gpu->stream, a);
+            if (masked)
+                hipLaunchKernelGGL(HK_FLASH(true, true), dim3(tail * pieces),
+                                   dim3(HK_THREADS), HK_ATTN_LDS, gpu->stream,
+                                   a);
+            else
+                hipLaunchKernelGGL(HK_FLASH(false, true), dim3(tail * pieces),
+                                   dim3(HK_THREADS), HK_ATTN_LDS, gpu->stream,
+                                   a);
             hipLaunchKernelGGL(hk_flash_combine, dim3(tail * 32), dim3(256),
                                0, gpu->stream, a);
         }

@@ -67,6 +67,35 @@ def test_sparse_sdpa_matches_oracle(gpu, rows, heads, head_major):
         clear(gpu)
 
 
+def test_sparse_split_pieces_with_empty_block(gpu):
+    """700 rows, 2 heads: 6 work items on 256 CUs, so each is cut into
+    key-range pieces; query block 2 keeps no tile at all (its rows are
+    zeros, as in the reference) and block 4 only the last tile (most of its
+    pieces are empty)."""
+    rows, heads, hd = 700, 2, 128
+    rng = np.random.default_rng(41)
+    q, k, v = (rand_bf16(rng, rows * heads * hd) for _ in range(3))
+    lists = [[0, 3, 7], [1, 2, 10], [], [4, 5, 6, 9], [10], [0, 10]]
+    ptr, idx = [0], []
+    for tiles in lists:
+        idx += tiles
+        ptr.append(len(idx))
+    assert register(gpu, ptr, idx, rows), gpu.error()
+    try:
+        out = gpu.new_bf16(rows * heads * hd)
+        scale = 1.0 / math.sqrt(hd)
+        gpu.run("h3_gpu_sdpa_bf16", out, gpu.bf16(q), gpu.bf16(k),
+                gpu.bf16(v), rows, heads, hd, C.c_float(scale))
+        got = gpu.read_bf16(out)
+        want = oracle.sdpa_sparse(q, k, v, rows, heads, hd, scale, ptr, idx)
+        assert not got.reshape(rows, -1)[256:384].any()
+        assert_close(got, want, what="sparse SDPA, split pieces",
+                     extra_abs=2 * sdpa_p_rounding_bound(
+                         q, k, v, rows, rows, heads, hd, scale))
+    finally:
+        clear(gpu)
+
+
 def test_mask_only_applies_to_its_row_count(gpu):
     """Other sequence lengths and cross attention stay dense; clearing the
     mask restores dense attention."""
