@@ -504,44 +504,76 @@ hk_gemm_mfma(hk_gemm_args g) {
 
 /* Skinny GEMM for M <= 64 rows (the per-block modulation projections:
  * time rows x 2688 against 96768 x 2688 weights).  Bound by streaming W
- * from HBM once, so no LDS and no W re-reads: each wave owns 32 W rows
- * (output columns) and all MB x 32 rows of X, and reads its MFMA fragments
- * straight from global memory (16 bytes per lane).  The W fragments of the
- * next D - 1 64-wide k steps are in flight while one step's MFMAs run (the
- * stream is latency-bound otherwise); X is small, stays in L2 and is
- * fetched one step ahead.  The step's k offset goes in the buffer's scalar
- * offset; rows past M or N keep a lane offset beyond the buffer and read
- * zeros. */
+ * from HBM once, so W never touches LDS and is never re-read: each wave
+ * owns 32 W rows (output columns) and reads their MFMA fragments straight
+ * from global memory (16 bytes per lane), D - 1 64-wide k steps ahead of
+ * the MFMAs.  X (MB x 32 rows) is shared by the workgroup's four waves:
+ * one DMA load per thread and step stages it into LDS (double-buffered,
+ * 128-byte rows with the 16-byte-chunk swizzle of the big GEMM), so L2
+ * serves it once per workgroup instead of once per wave.  The step's k
+ * offset goes in the buffer's scalar offset; rows past M or N keep a lane
+ * offset beyond the buffer and read zeros.
+ *
+ * Ordering: the prologue issues W(0), W(1), X(0), W(2); step s waits until
+ * at most the 4 loads of W(s+2) are outstanding (loads retire in order, so
+ * X(s) and W(s) have landed), synchronises, stages X(s+1) into the buffer
+ * every wave finished reading in step s-1, issues W(s+3) and computes. */
+/* One 64-wide k step of X rows into an LDS stage: thread tid's MB
+ * direct-to-LDS loads fill slots 256 i + tid. */
+template <int MB>
+__device__ __forceinline__ void hk_skinny_stage_x(
+    __amdgpu_buffer_rsrc_t xr, uint8_t *stage, const uint32_t *xo,
+    uint32_t wave, uint32_t step) {
+#pragma unroll
+    for (int i = 0; i < MB; i++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            xr,
+            (__attribute__((address_space(3))) void *)(
+                stage + (256u * i + wave * 64u) * 16u),
+            16, xo[i], step * 128u, 0, 0);
+}
+
 template <int MB>
 __global__ void __launch_bounds__(256)
 hk_gemm_skinny(const uint16_t *x, const uint16_t *w, const uint16_t *bias,
                uint16_t *c, uint32_t m, uint32_t n, uint32_t k,
                uint32_t x_bytes, uint32_t w_bytes) {
     constexpr int D = 4;
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    constexpr uint32_t XSTAGE = MB * 32u * 128u; /* bytes of X per k step */
+    /* two X stages, 2 XSTAGE bytes of dynamic LDS */
+    extern __shared__ __attribute__((aligned(16))) uint8_t hk_xs[];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t row = lane & 31u, half = lane >> 5;
     const uint32_t n0 = (blockIdx.x * 4u + wave) * 32u;
     const __amdgpu_buffer_rsrc_t xr = hk_rsrc(x, x_bytes);
     const __amdgpu_buffer_rsrc_t wr = hk_rsrc(w, w_bytes);
     const uint32_t wo = (min(n0 + row, n) * k + half * 8u) * 2u;
+    /* X staging: slot p = 256 i + tid holds row p / 8, physical chunk p % 8
+     * = logical chunk (p % 8) ^ key(row) */
     uint32_t xo[MB];
 #pragma unroll
-    for (int mb = 0; mb < MB; mb++)
-        xo[mb] = (min(mb * 32u + row, m) * k + half * 8u) * 2u;
-    hk_v4i wf[D][4], xf[2][MB][4];
+    for (int i = 0; i < MB; i++) {
+        const uint32_t p = 256u * i + tid, r = p >> 3;
+        const uint32_t chunk = (p & 7u) ^ hk_swz_key(r);
+        xo[i] = (min(r, m) * k + chunk * 8u) * 2u;
+    }
+    auto stage_x = [&](int buf, uint32_t step) {
+        hk_skinny_stage_x<MB>(xr, hk_xs + buf * XSTAGE, xo, wave, step);
+    };
+    hk_v4i wf[D][4];
     auto load_w = [&](int slot, uint32_t step) {
 #pragma unroll
         for (int q = 0; q < 4; q++)
             wf[slot][q] = __builtin_amdgcn_raw_buffer_load_b128(
                 wr, wo, step * 128u + q * 32u, 0);
     };
-    auto load_x = [&](int slot, uint32_t step) {
-#pragma unroll
-        for (int mb = 0; mb < MB; mb++)
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-                xf[slot][mb][q] = __builtin_amdgcn_raw_buffer_load_b128(
-                    xr, xo[mb], step * 128u + q * 32u, 0);
+    /* fragment of X rows mb*32 + row, logical chunk 2q + half */
+    auto read_x = [&](int buf, int mb, int q) {
+        const uint32_t r = mb * 32u + row;
+        return *(const hk_bf16x8 *)(
+            hk_xs + buf * XSTAGE + r * 128u +
+            (((2u * q + half) ^ hk_swz_key(r)) << 4));
     };
     hk_f32x16 acc[MB];
 #pragma unroll
@@ -549,25 +581,29 @@ hk_gemm_skinny(const uint16_t *x, const uint16_t *w, const uint16_t *bias,
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[mb][r] = 0.0f;
     const uint32_t steps = k / 64u;
-#pragma unroll
-    for (int d = 0; d < D - 1; d++)
-        if ((uint32_t)d < steps) load_w(d, d);
-    load_x(0, 0);
+    load_w(0, 0);
+    if (steps > 1) load_w(1, 1);
+    stage_x(0, 0);
+    if (steps > 2) load_w(2, 2);
     for (uint32_t s0 = 0; s0 < steps; s0 += D) {
 #pragma unroll
         for (int d = 0; d < D; d++) {
             const uint32_t s = s0 + d;
             if (s >= steps) break;
-            if (s + D - 1 < steps) load_w((d + D - 1) % D, s + D - 1);
-            if (s + 1 < steps) load_x((d + 1) & 1, s + 1);
+            if (s + 2 < steps)
+                asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+            else
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (s + 1 < steps) stage_x((d + 1) & 1, s + 1);
+            if (s + 3 < steps) load_w((d + 3) % D, s + 3);
 #pragma unroll
             for (int q = 0; q < 4; q++)
 #pragma unroll
                 for (int mb = 0; mb < MB; mb++)
                     acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                         __builtin_bit_cast(hk_bf16x8, wf[d][q]),
-                        __builtin_bit_cast(hk_bf16x8, xf[d & 1][mb][q]),
-                        acc[mb], 0, 0, 0);
+                        read_x(d & 1, mb, q), acc[mb], 0, 0, 0);
         }
     }
     /* acc[mb][r] = C[mb*32 + row][n0 + (r/4)*8 + half*4 + r%4] */
@@ -763,12 +799,14 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
     if (mfma && m <= 64 && epilogue == HK_EPI_STORE) {
         if (m <= 32)
             hipLaunchKernelGGL(hk_gemm_skinny<1>, dim3((n + 127) / 128),
-                               dim3(256), 0, gpu->stream, x, w, bias, c, m, n,
-                               k, (uint32_t)x_bytes, (uint32_t)w_bytes);
+                               dim3(256), 2 * 32 * 128, gpu->stream, x, w,
+                               bias, c, m, n, k, (uint32_t)x_bytes,
+                               (uint32_t)w_bytes);
         else
             hipLaunchKernelGGL(hk_gemm_skinny<2>, dim3((n + 127) / 128),
-                               dim3(256), 0, gpu->stream, x, w, bias, c, m, n,
-                               k, (uint32_t)x_bytes, (uint32_t)w_bytes);
+                               dim3(256), 2 * 64 * 128, gpu->stream, x, w,
+                               bias, c, m, n, k, (uint32_t)x_bytes,
+                               (uint32_t)w_bytes);
         return 1;
     }
     if (mfma) {
