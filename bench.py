@@ -169,9 +169,18 @@ def h3_measure(gpu, blocks, reps, latent_h=32, latent_w=32, full=True):
         hdit.sampler_init_random(seed=2, weight_std=0.02, mod_std=0.1)
         # modulation of all 39 time rows from the random-init time MLP and
         # adaLN projections (reference h3_dit_schedule.c:78-337)
-        t0 = time.perf_counter()
+        # device time of the precompute's own ops; the random-init fills of
+        # its (synthetic) projection weights are timed apart
+        L.h3_hip_op_timing_enable(gpu.h, 1)
+        L.h3_hip_op_timing_reset(gpu.h)
         hdit.schedule_precompute(seed=3, weight_std=0.02)
-        precompute_s = time.perf_counter() - t0
+        counts, all_ms, fill_ms = C.c_uint64(), C.c_double(), C.c_double()
+        L.h3_hip_op_timing_read(gpu.h, b"", C.byref(counts), C.byref(all_ms))
+        L.h3_hip_op_timing_read(gpu.h, b"fill_normal", C.byref(counts),
+                                C.byref(fill_ms))
+        L.h3_hip_op_timing_enable(gpu.h, 0)
+        precompute_s = (all_ms.value - fill_ms.value) / 1e3
+        precompute_fill_s = fill_ms.value / 1e3
         # forward alone, on the step-0 modulation rows
         hdit.gpu.begin()
         if not L.h3hip_dit_forward_step(hdit.h, 0):
@@ -208,7 +217,8 @@ def h3_measure(gpu, blocks, reps, latent_h=32, latent_w=32, full=True):
                "steps": steps, "fresh_forwards": int(evaluations),
                "seconds": round(seconds, 3),
                "s_per_fresh_forward": round(seconds / evaluations, 4),
-               "schedule_precompute_s": round(precompute_s, 3),
+               "schedule_precompute_s": round(precompute_s, 4),
+               "schedule_weight_fill_s": round(precompute_fill_s, 4),
                "time_rows": int(time_rows)}
     finally:
         hdit.close()
