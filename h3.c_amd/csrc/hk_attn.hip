@@ -524,7 +524,9 @@ __global__ void __launch_bounds__(256) hk_flash_combine(hk_attn_args a) {
                                       hk_pack2(sum.z * inv, sum.w * inv));
 }
 
-static bool hk_attn_lds_ready = false;
+/* devices (bit = ordinal) whose attention kernels have their LDS limit
+ * raised */
+static uint64_t hk_attn_lds_ready = 0;
 /* the comma in a template argument list confuses hipLaunchKernelGGL */
 #define HK_FLASH(sparse, split) (hk_flash_fwd<sparse, split>)
 
@@ -549,7 +551,8 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
                        ((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0 &&
                        ((uintptr_t)v & 15) == 0 && ((uintptr_t)o & 7) == 0;
     if (flash) {
-        if (!hk_attn_lds_ready) {
+        const uint64_t lds_bit = 1ull << (gpu->device & 63);
+        if (!(hk_attn_lds_ready & lds_bit)) {
             (void)hipFuncSetAttribute(
                 (const void *)hk_flash_fwd<false, false>,
                 hipFuncAttributeMaxDynamicSharedMemorySize, HK_ATTN_LDS);
@@ -562,7 +565,7 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
             (void)hipFuncSetAttribute(
                 (const void *)hk_flash_fwd<true, true>,
                 hipFuncAttributeMaxDynamicSharedMemorySize, HK_ATTN_LDS);
-            hk_attn_lds_ready = true;
+            hk_attn_lds_ready |= lds_bit;
         }
         hk_attn_args a;
         a.q = q; a.k = k; a.v = v; a.o = o;

@@ -659,7 +659,9 @@ __global__ void hk_swiglu_rows(const uint16_t *fused, uint16_t *out,
     out[index] = hk_f2bf(hk_silu_f(gate) * up);
 }
 
-static bool hk_gemm_lds_ready = false;
+/* devices (bit = ordinal) whose GEMM kernels have their LDS limit raised:
+ * the attribute is set with the device current, once per device */
+static uint64_t hk_gemm_lds_ready = 0;
 
 /* Split-K reduction over the tile-local partials: 4 tile rows per
  * workgroup, 4 columns per thread; C = epilogue(bf16 rounding of
@@ -769,8 +771,9 @@ static bool hk_gemm_mfma_ok(const struct h3_gpu *gpu, const void *x,
            ((uintptr_t)c & 7) == 0 && ((uintptr_t)bias & 7) == 0;
 }
 
-static void hk_gemm_lds_setup() {
-    if (hk_gemm_lds_ready) return;
+static void hk_gemm_lds_setup(const struct h3_gpu *gpu) {
+    const uint64_t bit = 1ull << (gpu->device & 63);
+    if (hk_gemm_lds_ready & bit) return;
     (void)hipFuncSetAttribute((const void *)hk_gemm_mfma<HK_EPI_STORE>,
                               hipFuncAttributeMaxDynamicSharedMemorySize,
                               HK_GEMM_LDS);
@@ -786,7 +789,7 @@ static void hk_gemm_lds_setup() {
     (void)hipFuncSetAttribute(
         (const void *)hk_gemm_mfma<HK_EPI_PARTIAL_SWIGLU>,
         hipFuncAttributeMaxDynamicSharedMemorySize, HK_GEMM_LDS);
-    hk_gemm_lds_ready = true;
+    hk_gemm_lds_ready |= bit;
 }
 
 int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
@@ -810,7 +813,7 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
         return 1;
     }
     if (mfma) {
-        hk_gemm_lds_setup();
+        hk_gemm_lds_setup(gpu);
         hk_gemm_args g;
         g.x = x; g.w = w; g.bias = bias; g.c = c;
         g.m = m; g.n = n; g.k = k;
@@ -941,7 +944,7 @@ int hk_gemm_bf16_pair(struct h3_gpu *gpu, const uint16_t *x,
     if (!paired)
         return hk_gemm_bf16(gpu, x, w0, b0, c0, m, n, k, HK_EPI_STORE) &&
                hk_gemm_bf16(gpu, x, w1, b1, c1, m, n, k, HK_EPI_STORE);
-    hk_gemm_lds_setup();
+    hk_gemm_lds_setup(gpu);
     hk_gemm_args g;
     g.x = x; g.w = w0; g.bias = b0; g.c = c0;
     g.m = m; g.n = n; g.k = k;
