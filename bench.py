@@ -37,25 +37,8 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def wan_positions(t, h, w):
-    """(t, h, w) integer grid of the video tokens, row-major."""
-    tt, hh, ww = np.meshgrid(np.arange(t), np.arange(h), np.arange(w),
-                             indexing="ij")
-    pos = np.stack([tt.ravel(), hh.ravel(), ww.ravel()], axis=1)
-    return pos.astype(np.float64)
-
-
-def rope_tables(positions):
-    L = h3hip.lib()
-    rows = positions.shape[0]
-    inv = np.empty(16, np.float32)
-    L.h3hip_default_inv_freq(h3hip.ptr(inv))
-    pos = np.ascontiguousarray(positions, dtype=np.float64)
-    cos = np.empty(rows * 48, np.float32)
-    sin = np.empty(rows * 48, np.float32)
-    L.h3hip_rope_tables(h3hip.ptr(pos), rows, h3hip.ptr(inv), 1.0,
-                        h3hip.ptr(cos), h3hip.ptr(sin))
-    return cos, sin
+wan_positions = h3hip.wan_positions
+rope_tables = h3hip.rope_tables
 
 
 def time_forward(gpu, dit, blocks, steps, warmup):

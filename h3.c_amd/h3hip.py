@@ -570,6 +570,30 @@ def dit_config(family, hidden, heads, ffn, rows, blocks=1, text_rows=0,
                      text_rows, time_rows, rope_half, epsilon)
 
 
+def wan_positions(t, h, w):
+    """(t, h, w) integer grid of the video tokens in row-major token order
+    (the patchified latent's order), as float64 [rows][3]."""
+    tt, hh, ww = np.meshgrid(np.arange(t), np.arange(h), np.arange(w),
+                             indexing="ij")
+    pos = np.stack([tt.ravel(), hh.ravel(), ww.ravel()], axis=1)
+    return pos.astype(np.float64)
+
+
+def rope_tables(positions, scale=1.0):
+    """3D RoPE cos/sin tables [rows][48] (F32) for the given positions, from
+    the backend's host math (h3hip_rope_tables, the reference's
+    prepare_rope table, h3_dit.c:907-922)."""
+    L = lib()
+    rows = positions.shape[0]
+    inv = np.empty(16, np.float32)
+    L.h3hip_default_inv_freq(ptr(inv))
+    pos = np.ascontiguousarray(positions, dtype=np.float64)
+    cos = np.empty(rows * 48, np.float32)
+    sin = np.empty(rows * 48, np.float32)
+    L.h3hip_rope_tables(ptr(pos), rows, ptr(inv), scale, ptr(cos), ptr(sin))
+    return cos, sin
+
+
 def block_flops(cfg):
     """FLOPs of one block (host math only, no device needed)."""
     return lib().h3hip_dit_block_flops(C.byref(cfg))

@@ -357,45 +357,68 @@ void orc_qkv_rope(const bf16 *qkv, const bf16 *qw, const bf16 *kw,
 void orc_sdpa(const bf16 *q, const bf16 *k, const bf16 *v, bf16 *out,
               size_t q_rows, size_t kv_rows, size_t heads, size_t hd,
               float scale, int head_major, int round_p) {
-#pragma omp parallel
-    {
-        float *s = (float *)malloc((kv_rows ? kv_rows : 1) * sizeof(float));
-        float *qf = (float *)malloc(hd * sizeof(float));
-        float *acc = (float *)malloc(hd * sizeof(float));
-#pragma omp for schedule(dynamic, 4)
-        for (size_t i = 0; i < q_rows * heads; i++) {
-            const size_t row = i / heads, head = i % heads;
-            const size_t qb = (row * heads + head) * hd;
-            for (size_t d = 0; d < hd; d++) qf[d] = b2f(q[qb + d]);
-            float mx = -INFINITY;
-            for (size_t j = 0; j < kv_rows; j++) {
-                const bf16 *kr = k + (j * heads + head) * hd;
-                float dot = 0.0f;
-                for (size_t d = 0; d < hd; d++) dot = fmaf(qf[d], b2f(kr[d]), dot);
-                s[j] = dot * scale;
-                if (s[j] > mx) mx = s[j];
+    /* One head at a time: its K is widened once into a [hd][kv_rows]
+     * transpose and V into [kv_rows][hd], so the score loop runs over keys
+     * with d outermost.  Each score is still the sequential fmaf chain over
+     * d = 0..hd-1 from 0, so the result does not depend on the layout. */
+    const size_t kv = kv_rows ? kv_rows : 1;
+    float *kt = (float *)malloc(hd * kv * sizeof(float));
+    float *vf = (float *)malloc(kv * hd * sizeof(float));
+    for (size_t head = 0; head < heads; head++) {
+#pragma omp parallel for schedule(static)
+        for (size_t j = 0; j < kv_rows; j++) {
+            const bf16 *kr = k + (j * heads + head) * hd;
+            const bf16 *vr = v + (j * heads + head) * hd;
+            for (size_t d = 0; d < hd; d++) {
+                kt[d * kv_rows + j] = b2f(kr[d]);
+                vf[j * hd + d] = b2f(vr[d]);
             }
-            float l = 0.0f;
-            for (size_t j = 0; j < kv_rows; j++) {
-                s[j] = expf(s[j] - mx);
-                l += s[j];
-            }
-            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-            for (size_t d = 0; d < hd; d++) acc[d] = 0.0f;
-            for (size_t j = 0; j < kv_rows; j++) {
-                const bf16 *vr = v + (j * heads + head) * hd;
-                const float p = round_p ? rbf(s[j]) : s[j] * inv;
-                for (size_t d = 0; d < hd; d++)
-                    acc[d] = fmaf(p, b2f(vr[d]), acc[d]);
-            }
-            const size_t ob = head_major ? (head * q_rows + row) * hd : qb;
-            for (size_t d = 0; d < hd; d++)
-                out[ob + d] = f2b(round_p ? acc[d] * inv : acc[d]);
         }
-        free(s);
-        free(qf);
-        free(acc);
+#pragma omp parallel
+        {
+            float *s = (float *)malloc(kv * sizeof(float));
+            float *qf = (float *)malloc(hd * sizeof(float));
+            float *acc = (float *)malloc(hd * sizeof(float));
+#pragma omp for schedule(dynamic, 4)
+            for (size_t row = 0; row < q_rows; row++) {
+                const size_t qb = (row * heads + head) * hd;
+                for (size_t d = 0; d < hd; d++) qf[d] = b2f(q[qb + d]);
+                for (size_t j = 0; j < kv_rows; j++) s[j] = 0.0f;
+                for (size_t d = 0; d < hd; d++) {
+                    const float qd = qf[d];
+                    const float *kd = kt + d * kv_rows;
+                    for (size_t j = 0; j < kv_rows; j++)
+                        s[j] = fmaf(qd, kd[j], s[j]);
+                }
+                float mx = -INFINITY;
+                for (size_t j = 0; j < kv_rows; j++) {
+                    s[j] *= scale;
+                    if (s[j] > mx) mx = s[j];
+                }
+                float l = 0.0f;
+                for (size_t j = 0; j < kv_rows; j++) {
+                    s[j] = expf(s[j] - mx);
+                    l += s[j];
+                }
+                const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+                for (size_t d = 0; d < hd; d++) acc[d] = 0.0f;
+                for (size_t j = 0; j < kv_rows; j++) {
+                    const float *vr = vf + j * hd;
+                    const float p = round_p ? rbf(s[j]) : s[j] * inv;
+                    for (size_t d = 0; d < hd; d++)
+                        acc[d] = fmaf(p, vr[d], acc[d]);
+                }
+                const size_t ob = head_major ? (head * q_rows + row) * hd : qb;
+                for (size_t d = 0; d < hd; d++)
+                    out[ob + d] = f2b(round_p ? acc[d] * inv : acc[d]);
+            }
+            free(s);
+            free(qf);
+            free(acc);
+        }
     }
+    free(kt);
+    free(vf);
 }
 
 /* Block-sparse joint attention (reference h3_gpu.h:44-52, the FA2 kernel's

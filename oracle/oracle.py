@@ -442,12 +442,18 @@ def h3_forward_step(m, step):
     return video, audio
 
 
-def h3_denoise(m, video_sigmas, audio_sigmas, reuse_interval):
+def h3_denoise(m, video_sigmas, audio_sigmas, reuse_interval,
+               forward=None):
     """The GPU Euler loop with velocity reuse (h3_dit.c:2745-2917): cache
     the previous velocity before each fresh evaluation, extrapolate on the
     skipped steps, x += (sigma_i - sigma_i+1) (v + r (v - v_prev)).
+    `forward(m, step) -> (video, audio)` evaluates the velocities (default:
+    h3_forward_step, the oracle's own forward; a test may pass the device's
+    forward to check the loop alone at sizes the oracle forward cannot run).
     Returns the updated (video, audio) F32 latent rows and the number of
     evaluations."""
+    if forward is None:
+        forward = h3_forward_step
     steps = len(video_sigmas) - 1
     vp, ac = m["video_patch"], m["audio_channels"]
     video = np.array(m["video_input"], np.float32)
@@ -464,7 +470,7 @@ def h3_denoise(m, video_sigmas, audio_sigmas, reuse_interval):
                 vprev, aprev = vv.copy(), av.copy()
                 previous = last
             mm = dict(m, video_input=video, audio_input=audio)
-            vv, av = h3_forward_step(mm, step)
+            vv, av = forward(mm, step)
             last = step
             evaluations += 1
         have = previous >= 0

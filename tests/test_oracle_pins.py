@@ -448,6 +448,122 @@ def test_h3_blocks_zero_gates_leave_residual():
     np.testing.assert_array_equal(out, x)
 
 
+def _wiring_block(d, heads, ffn, T, mode, mod_seed):
+    """One H3 block whose weights make one branch a closed form of its adaLN
+    input (hidden = heads * 128, ffn = hidden):
+      mode "attn": q and k projections 0 (uniform softmax), v projection and
+        out-projection the identity, so the attention branch returns the row
+        mean of its adaLN output; attention gate 1, MLP gate 0;
+      mode "mlp": attention gate 0, fc1 = [4 I ; I] (gate rows, up rows),
+        fc2 = I, so the MLP branch is swiglu([4 a, a]) of its adaLN output a;
+        MLP gate 1;
+      mode "skip": both gates 0 (the block returns its input).
+    norm1, norm2 and all modulation slots are distinct random values."""
+    r = np.random.default_rng(mod_seed)
+    hd = 128
+    inner = heads * hd
+    mod = 0.5 * r.standard_normal((T, 3, 6, d))
+    mod[:, :, 2] = 1.0 if mode == "attn" else 0.0
+    mod[:, :, 5] = 1.0 if mode == "mlp" else 0.0
+    qkv = np.zeros((heads, 3, hd, d))
+    for h in range(heads):
+        qkv[h, 2, :, h * hd:(h + 1) * hd] = np.eye(hd)
+    fc1 = np.concatenate([4.0 * np.eye(ffn, d), np.eye(ffn, d)])
+    return {"norm1": b(1.0 + 0.5 * r.standard_normal(d)),
+            "norm2": b(1.0 + 0.5 * r.standard_normal(d)),
+            "qkv": b(qkv.ravel()), "q_norm": b(np.ones(hd)),
+            "k_norm": b(np.ones(hd)), "out": b(np.eye(d, inner).ravel()),
+            "fc1": b(fc1.ravel()), "fc2": b(np.eye(d, ffn).ravel()),
+            "modulation": b(mod.ravel())}
+
+
+def _wiring_setup(rows=24, d=256, heads=2, T=3):
+    r = np.random.default_rng(77)
+    x = b(r.standard_normal(rows * d))
+    row_map = r.integers(0, 3 * T, rows).astype(np.uint32)
+    ang = r.uniform(-3, 3, rows * 48)
+    return x, row_map, b(np.cos(ang)), b(np.sin(ang))
+
+
+def _attn_closed_form(x, w, row_map, rows, d, shift, scale, norm):
+    """x + mean over rows of adaln(x; norm, slots shift/scale), the value the
+    "attn" wiring block must produce, in float64."""
+    a = oracle.adaln(x, w[norm], w["modulation"], row_map, rows, d, 6, shift,
+                     scale, 1e-5)
+    y = f64(a).reshape(rows, d).mean(axis=0)
+    return f64(x).reshape(rows, d) + y[None, :], y
+
+
+def _assert_attn_wiring(got, x, w, row_map, rows, d):
+    want, y = _attn_closed_form(x, w, row_map, rows, d, 0, 1, "norm1")
+    g = f64(got).reshape(rows, d)
+    # bf16 rounding of the mean and of the residual sum
+    tol = 2.0 ** -8 * (np.abs(y)[None, :] + np.abs(want)) + 1e-30
+    assert (np.abs(g - want) <= tol).all(), float(np.abs(g - want).max())
+    # the check has the power to see a swapped slot pair or norm weight
+    for shift, scale, norm in ((1, 0, "norm1"), (0, 1, "norm2"),
+                               (3, 4, "norm1")):
+        wrong, _ = _attn_closed_form(x, w, row_map, rows, d, shift, scale,
+                                     norm)
+        assert (np.abs(g - wrong) > tol).any()
+
+
+def test_h3_block_attention_branch_wiring():
+    """The attention branch reads adaLN(x; norm1, shift slot 0, scale slot 1)
+    of the block's own modulation row (row_map[r]) and is added through gate
+    slot 2 (h3_dit.c:2030-2032 adaLN, :2100-2105 gate).  With q = k = 0 and
+    identity v / out projections the branch is the row mean of that adaLN
+    output, so the block output is x + mean(adaLN(x)) up to two bf16
+    roundings; slots 1/0, norm2 or slots 3/4 in its place fail."""
+    rows, d, heads = 24, 256, 2
+    x, row_map, cos, sin = _wiring_setup(rows, d, heads)
+    w = _wiring_block(d, heads, d, 3, "attn", 5)
+    got = oracle.h3_blocks(x, [w], row_map, cos, sin, rows, d, heads, d)
+    _assert_attn_wiring(got, x, w, row_map, rows, d)
+
+
+def test_h3_block_mlp_branch_wiring():
+    """The MLP branch reads adaLN(x; norm2, shift slot 3, scale slot 4) and
+    is added through gate slot 5 (h3_dit.c:2100-2105 gate + adaLN,
+    :2139-2177 MLP gate).  With the attention gate at 0 and fc1 = [4I ; I],
+    fc2 = I the block output is gate(x, swiglu([4a, a]), slot 5) with
+    a = adaLN(x) -- bit for bit, since every step in between is exact; slots
+    4/3, norm1 or slots 0/1 in its place fail."""
+    rows, d, heads = 24, 256, 2
+    x, row_map, cos, sin = _wiring_setup(rows, d, heads)
+    w = _wiring_block(d, heads, d, 3, "mlp", 6)
+    got = oracle.h3_blocks(x, [w], row_map, cos, sin, rows, d, heads, d)
+
+    def closed(shift, scale, norm):
+        a = oracle.adaln(x, w[norm], w["modulation"], row_map, rows, d, 6,
+                         shift, scale, 1e-5).reshape(rows, d)
+        fused = np.concatenate([b(4.0 * f64(a)), a], axis=1)
+        m = oracle.swiglu(fused.ravel(), rows, d)
+        return oracle.gate(x, m, w["modulation"], row_map, rows, d, 6, 5)
+
+    np.testing.assert_array_equal(got, closed(3, 4, "norm2"))
+    for wrong in ((4, 3, "norm2"), (3, 4, "norm1"), (0, 1, "norm2")):
+        assert not np.array_equal(got, closed(*wrong))
+
+
+def test_h3_blocks_fused_adaln_takes_the_next_blocks_weights():
+    """The MLP gate of block i is fused with block i+1's attention adaLN,
+    which must use block i+1's norm1 and modulation (h3_dit.c:2139-2178).
+    Block 0 is a pass-through (both gates 0, so its output is its input bit
+    for bit) with its own distinct norm1 / modulation; block 1 is the
+    attention-wiring block.  The two-block output must be the closed form of
+    block 1 alone; block 0's weights in the fused adaLN fail it."""
+    rows, d, heads = 24, 256, 2
+    x, row_map, cos, sin = _wiring_setup(rows, d, heads)
+    w0 = _wiring_block(d, heads, d, 3, "skip", 8)
+    w1 = _wiring_block(d, heads, d, 3, "attn", 9)
+    got = oracle.h3_blocks(x, [w0, w1], row_map, cos, sin, rows, d, heads, d)
+    _assert_attn_wiring(got, x, w1, row_map, rows, d)
+    wrong, y = _attn_closed_form(x, w0, row_map, rows, d, 0, 1, "norm1")
+    tol = 2.0 ** -8 * (np.abs(y)[None, :] + np.abs(wrong))
+    assert (np.abs(f64(got).reshape(rows, d) - wrong) > tol).any()
+
+
 def test_bf16_rounding_is_rne():
     """RNE ties: 1 + 2^-8 is halfway between 1 and 1 + 2^-7 -> even (1);
     1 + 3 * 2^-8 -> 1 + 2^-6 (even mantissa)."""
