@@ -36,6 +36,8 @@
 #include "hk_common.h"
 #include "hk_internal.h"
 
+#include <pthread.h>
+
 #include <math.h>
 #include <stdlib.h>
 
@@ -794,7 +796,8 @@ static void hk_gemm_lds_setup(const struct h3_gpu *gpu) {
 
 int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
                  const uint16_t *bias, uint16_t *c, uint32_t m, uint32_t n,
-                 uint32_t k, int epilogue) {
+                 uint32_t k, int epilogue, float *scratch,
+                 size_t scratch_bytes) {
     if (!m || !n) return 1;
     const uint64_t w_rows = epilogue == HK_EPI_SWIGLU ? 2ull * n : n;
     const uint64_t x_bytes = (uint64_t)m * k * 2, w_bytes = w_rows * k * 2;
@@ -847,8 +850,16 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
             uint32_t splits = min(cus / tail, k_steps / 4);
             const uint32_t steps = (k_steps + splits - 1) / splits;
             splits = (k_steps + steps - 1) / steps;
-            float *partial = (float *)hk_splitk_space(
-                gpu, (size_t)splits * tail * HK_BM * HK_BN * 4);
+            const size_t partial_bytes =
+                (size_t)splits * tail * HK_BM * HK_BN * 4;
+            if (scratch && partial_bytes > scratch_bytes)
+                return hk_fail(gpu,
+                               "linear needs %zu bytes of split-K scratch, "
+                               "over the %zu-byte static maximum",
+                               partial_bytes, scratch_bytes);
+            float *partial = scratch ? scratch
+                                     : (float *)hk_splitk_space(
+                                           gpu, partial_bytes);
             if (!partial) return 0;
             if (full) {
                 g.tile_count = full;
@@ -973,6 +984,52 @@ int hk_gemm_bf16_pair(struct h3_gpu *gpu, const uint16_t *x,
     return 1;
 }
 
+/* ================================================== allocation-free linear
+ *
+ * h3_hip_linear_bf16_noalloc's split-K partials live in this file-scope
+ * device array instead of the context's on-demand scratch, so the call
+ * makes no allocation.  Each device holds its own copy from the library's
+ * load until the process ends; its address on a device comes from
+ * hipGetSymbolAddress (the host-side name is only a stand-in and must never
+ * reach a kernel), looked up once per device with that device current.
+ * The partial tiles are written in full by the split pieces before the
+ * reduction reads them, so the array needs no clearing between calls; calls
+ * that overlap on one device share it and race. */
+#define HK_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+static __device__ __align__(256) float
+    scratch[HK_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+static float *hk_scratch_ptr[64];
+static pthread_mutex_t hk_scratch_lock = PTHREAD_MUTEX_INITIALIZER;
+
+static float *hk_noalloc_scratch(struct h3_gpu *gpu) {
+    if (gpu->device < 0 || gpu->device >= 64) {
+        hk_fail(gpu, "device ordinal %d out of range", gpu->device);
+        return NULL;
+    }
+    pthread_mutex_lock(&hk_scratch_lock);
+    float *ptr = hk_scratch_ptr[gpu->device];
+    if (!ptr) {
+        int current = -1;
+        hipError_t status = hipGetDevice(&current);
+        if (status == hipSuccess && current != gpu->device)
+            status = hipSetDevice(gpu->device);
+        if (status == hipSuccess)
+            status = hipGetSymbolAddress((void **)&ptr, HIP_SYMBOL(scratch));
+        if (current >= 0 && current != gpu->device)
+            (void)hipSetDevice(current);
+        if (status != hipSuccess || !ptr) {
+            pthread_mutex_unlock(&hk_scratch_lock);
+            hk_fail_hip(gpu, "static scratch address lookup",
+                        status != hipSuccess ? status : hipErrorUnknown);
+            return NULL;
+        }
+        hk_scratch_ptr[gpu->device] = ptr;
+    }
+    pthread_mutex_unlock(&hk_scratch_lock);
+    return ptr;
+}
+
 /* ================================================================ ops */
 
 extern "C" {
@@ -1000,6 +1057,32 @@ int h3_gpu_linear_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
     if (!hk_gemm_bf16(gpu, HK_CBF16(input), HK_CBF16(weight),
                       bias ? HK_CBF16(bias) : NULL, HK_BF16(output), rows,
                       output_dim, input_dim, HK_EPI_STORE))
+        return 0;
+    return hk_op_end(gpu, "gemm", hk_linear_kind(rows, input_dim, output_dim));
+}
+
+int h3_hip_linear_bf16_noalloc(h3_gpu *gpu, h3_gpu_tensor *output,
+                               const h3_gpu_tensor *input,
+                               const h3_gpu_tensor *weight,
+                               const h3_gpu_tensor *bias, uint32_t rows,
+                               uint32_t input_dim, uint32_t output_dim) {
+    if (!hk_require(gpu, input, (size_t)rows * input_dim, H3_GPU_BF16,
+                    "linear input") ||
+        !hk_require(gpu, weight, (size_t)output_dim * input_dim, H3_GPU_BF16,
+                    "linear weight") ||
+        !hk_require(gpu, output, (size_t)rows * output_dim, H3_GPU_BF16,
+                    "linear output") ||
+        (bias && !hk_require(gpu, bias, output_dim, H3_GPU_BF16,
+                             "linear bias")) ||
+        !hk_require_active(gpu))
+        return 0;
+    float *partial = hk_noalloc_scratch(gpu);
+    if (!partial) return 0;
+    hk_op_begin(gpu, "gemm");
+    if (!hk_gemm_bf16(gpu, HK_CBF16(input), HK_CBF16(weight),
+                      bias ? HK_CBF16(bias) : NULL, HK_BF16(output), rows,
+                      output_dim, input_dim, HK_EPI_STORE, partial,
+                      HK_NOALLOC_SCRATCH_BYTES))
         return 0;
     return hk_op_end(gpu, "gemm", hk_linear_kind(rows, input_dim, output_dim));
 }

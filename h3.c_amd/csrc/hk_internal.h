@@ -63,6 +63,8 @@ struct h3_gpu {
     uint32_t sparse_rows;
     /* file loader: pinned staging slots, copy stream, serialising lock */
     struct hk_loader *loader;
+    /* hipMalloc calls made for this context (tensors, scratch, masks) */
+    uint64_t device_mallocs;
 };
 
 /* stats kinds, mirroring the reference counters (h3_cuda_internal.h:142-160) */
@@ -135,10 +137,13 @@ enum { HK_EPI_STORE = 0, HK_EPI_SWIGLU = 1, HK_EPI_GELU = 2,
 
 /* C[M,N] = epi(A[M,K] . W[N,K]^T + bias).  For HK_EPI_SWIGLU the weight has
  * 2*N rows (gate rows [0,N), up rows [N,2N)) and C is the [M,N] activation.
- * ldc is the row stride of C in elements. */
+ * Split-K partials go to the context's scratch (grown on demand), or, when
+ * `scratch` is given, to that caller-owned device buffer of scratch_bytes:
+ * then nothing is allocated, and a split that needs more fails. */
 int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *a, const uint16_t *w,
                  const uint16_t *bias, uint16_t *c, uint32_t m, uint32_t n,
-                 uint32_t k, int epilogue);
+                 uint32_t k, int epilogue, float *scratch = nullptr,
+                 size_t scratch_bytes = 0);
 int hk_gemm_bf16_pair(struct h3_gpu *gpu, const uint16_t *x,
                       const uint16_t *w0, const uint16_t *b0, uint16_t *c0,
                       const uint16_t *w1, const uint16_t *b1, uint16_t *c1,

@@ -73,12 +73,14 @@ static void *hk_device_alloc(struct h3_gpu *gpu, size_t bytes) {
         link = &(*link)->next;
     }
     void *data = NULL;
+    gpu->device_mallocs++;
     hipError_t status = hipMalloc(&data, bytes);
     if (status != hipSuccess) {
         (void)hipGetLastError();
         /* release cached blocks and retry once */
         (void)hipStreamSynchronize(gpu->stream);
         hk_cache_evict(gpu, 0);
+        gpu->device_mallocs++;
         status = hipMalloc(&data, bytes);
         if (status != hipSuccess) {
             (void)hipGetLastError();
@@ -122,6 +124,7 @@ static void *hk_grow(struct h3_gpu *gpu, void **buffer, size_t *have,
     *buffer = NULL;
     *have = 0;
     void *fresh = NULL;
+    gpu->device_mallocs++;
     hipError_t status = hipMalloc(&fresh, capacity);
     if (status != hipSuccess) {
         (void)hipGetLastError();
@@ -259,6 +262,10 @@ extern "C" int h3_hip_op_timing_names(h3_gpu *gpu, char *buffer,
     for (auto &name : names) { joined += name; joined += '\n'; }
     snprintf(buffer, buffer_size, "%s", joined.c_str());
     return 1;
+}
+
+extern "C" uint64_t h3_hip_device_allocations(const h3_gpu *gpu) {
+    return gpu ? gpu->device_mallocs : 0;
 }
 
 extern "C" int h3_hip_marker(h3_gpu *gpu, int slot) {
@@ -469,6 +476,7 @@ extern "C" int h3_gpu_sdpa_set_sparse(h3_gpu *gpu, const uint32_t *ptr,
     for (size_t q = 0; q + 1 < ptr_count; q++)
         qsort(sorted + ptr[q], ptr[q + 1] - ptr[q], sizeof(uint32_t),
               hk_u32_compare);
+    gpu->device_mallocs += 2;
     int ok = hipMalloc((void **)&gpu->sparse_ptr,
                        ptr_count * sizeof(uint32_t)) == hipSuccess &&
              hipMalloc((void **)&gpu->sparse_idx,

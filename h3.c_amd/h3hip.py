@@ -126,6 +126,9 @@ def lib():
                                         _F]),
         "h3_hip_linear_pair_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _P,
                                          _U32, _U32, _U32]),
+        "h3_hip_linear_bf16_noalloc": (_I, [_P, _P, _P, _P, _P, _U32, _U32,
+                                            _U32]),
+        "h3_hip_device_allocations": (C.c_uint64, [_P]),
         "h3_gpu_layer_adaln_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _U32,
                                          _U32, _U32, _U32, _U32, _F]),
         "h3_gpu_gate_layer_adaln_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P,

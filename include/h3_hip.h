@@ -98,6 +98,20 @@ int h3_hip_linear_pair_bf16(h3_gpu *gpu, h3_gpu_tensor *output0,
                             const h3_gpu_tensor *bias1, uint32_t rows,
                             uint32_t input_dim, uint32_t output_dim);
 
+/* h3_gpu_linear_bf16 that allocates nothing: the same kernels and the same
+ * results, with the split-K partial tiles (used when the last round of
+ * 256x256 tiles would leave over half the CUs idle) in a static 64 MiB
+ * device array per GPU instead of the context's on-demand scratch.  A
+ * launch whose split would need more fails with an error naming the size.
+ * Calls that overlap on one GPU share that array and race.  No counterpart
+ * in the reference: it is for callers that cannot allocate device memory
+ * (HIP graph capture, fixed-footprint serving loops). */
+int h3_hip_linear_bf16_noalloc(h3_gpu *gpu, h3_gpu_tensor *output,
+                               const h3_gpu_tensor *input,
+                               const h3_gpu_tensor *weight,
+                               const h3_gpu_tensor *bias, uint32_t rows,
+                               uint32_t input_dim, uint32_t output_dim);
+
 /* output = bf16(gelu_tanh(bf16(X . W^T + b))): GEMM with the activation in
  * its epilogue. */
 int h3_gpu_linear_gelu_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
@@ -163,6 +177,12 @@ int h3_hip_op_timing_names(h3_gpu *gpu, char *buffer, size_t buffer_size);
 int h3_hip_marker(h3_gpu *gpu, int slot);
 int h3_hip_marker_elapsed(h3_gpu *gpu, int from_slot, int to_slot,
                           double *milliseconds);
+
+/* Number of device allocations (hipMalloc calls: tensors, op scratch,
+ * sparse masks) this context has made so far, cached-block reuse not
+ * counted.  Lets a caller that must not allocate inside a loop check that
+ * it did not. */
+uint64_t h3_hip_device_allocations(const h3_gpu *gpu);
 
 #ifdef __cplusplus
 }
