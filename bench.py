@@ -152,11 +152,15 @@ def h3_measure(gpu, blocks, reps, latent_h=32, latent_w=32, full=True):
         hdit.sampler_init_random(seed=2, weight_std=0.02, mod_std=0.1)
         # modulation of all 39 time rows from the random-init time MLP and
         # adaLN projections (reference h3_dit_schedule.c:78-337)
-        # device time of the precompute's own ops; the random-init fills of
-        # its (synthetic) projection weights are timed apart
+        # device time of the precompute's own ops (schedule_precompute_
+        # device_s); the random-init fills of its (synthetic) projection
+        # weights are timed apart; schedule_precompute_wall_s is the whole
+        # call's wall clock, fills, uploads, syncs and timing events included
         L.h3_hip_op_timing_enable(gpu.h, 1)
         L.h3_hip_op_timing_reset(gpu.h)
+        t0 = time.perf_counter()
         hdit.schedule_precompute(seed=3, weight_std=0.02)
+        precompute_wall_s = time.perf_counter() - t0
         counts, all_ms, fill_ms = C.c_uint64(), C.c_double(), C.c_double()
         L.h3_hip_op_timing_read(gpu.h, b"", C.byref(counts), C.byref(all_ms))
         L.h3_hip_op_timing_read(gpu.h, b"fill_normal", C.byref(counts),
@@ -200,7 +204,8 @@ def h3_measure(gpu, blocks, reps, latent_h=32, latent_w=32, full=True):
                "steps": steps, "fresh_forwards": int(evaluations),
                "seconds": round(seconds, 3),
                "s_per_fresh_forward": round(seconds / evaluations, 4),
-               "schedule_precompute_s": round(precompute_s, 4),
+               "schedule_precompute_device_s": round(precompute_s, 4),
+               "schedule_precompute_wall_s": round(precompute_wall_s, 4),
                "schedule_weight_fill_s": round(precompute_fill_s, 4),
                "time_rows": int(time_rows)}
     finally:
@@ -332,6 +337,18 @@ def load_traffic(name):
         return None
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or None."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(seconds_budget=30.0):
     """The CPU oracle on one Wan block at BASELINE config 1 (1536 video rows,
     256 text rows, hidden 5120); returns TFLOP/s and the sample used."""
@@ -368,7 +385,8 @@ def cpu_baseline(seconds_budget=30.0):
     flops = h3hip.block_flops(cfg)
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
     return {"value": round(flops / dt / 1e12, 4), "unit": "TFLOP/s",
-            "cores": threads, "kind": "port",
+            "cores": threads, "kind": "port", "cpu_model": cpu_model(),
+            "host_cpus": os.cpu_count(),
             "sample": (f"one Wan DiT block at BASELINE config 1 (1536 video "
                        f"+ 256 text rows, hidden 5120): {dt:.2f} s, "
                        f"{flops / 1e12:.3f} TFLOP; 50-block forward "

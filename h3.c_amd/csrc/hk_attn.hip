@@ -34,9 +34,9 @@
  *     VALU result hazards get their wait states), and the key-range mask
  *     is compiled only into the last tile's step.
  *
- * A two-pass reference kernel (the reference's naive SDPA,
- * h3_cuda_attention.cu:488-549: one workgroup per (row, head), normalised
- * F32 probabilities) serves other head sizes and H3_HIP_REFERENCE=1.
+ * A two-pass reference kernel (hk_attn_ref.hip, built with the default
+ * floating-point semantics) serves other head sizes, H3_HIP_REFERENCE=1 and
+ * the naive-SDPA knob.
  */
 #include "hk_common.h"
 #include "hk_internal.h"
@@ -286,8 +286,12 @@ __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
         /* online softmax per query column.  The running maximum is only
          * moved (and O, l rescaled) when a score exceeds it by more than
          * 2^8 in the exp2 domain; otherwise P = exp2(s - m_stale) <= 256.
-         * A power-of-two offset commutes with bf16 rounding, so P and the
-         * final O / l match an every-tile rescale up to f32 rounding. */
+         * The stale maximum is not the row's true maximum and the gap
+         * between them is not a power of two, so bf16(P) can round
+         * differently from the reference's P (relative to the row maximum)
+         * by up to half a bf16 ulp per element: O matches to the bf16
+         * rounding of P (the bound the tests apply), while l, summed over
+         * the unrounded P, is exact up to f32 rounding. */
         const uint32_t kv0 = tile * HK_KT;
         hk_bf16x8 pf[2][2][HK_QG]; /* [kt][step][g] */
 #pragma unroll
@@ -434,54 +438,6 @@ __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
                              o[d][g][blk * 4 + 3] * inv)};
                 *(uint2 *)(out + dim) = packed;
             }
-    }
-}
-
-/* Two-pass reference: one workgroup per (query row, head); scores in LDS. */
-__global__ void __launch_bounds__(256)
-hk_attn_reference(const uint16_t *q, const uint16_t *k, const uint16_t *v,
-                  uint16_t *o, uint32_t q_rows, uint32_t kv_rows,
-                  uint32_t heads, uint32_t head_dim, float scale,
-                  int head_major) {
-    extern __shared__ float scores[];
-    __shared__ float scratch[16];
-    const uint32_t row = blockIdx.x, head = blockIdx.y;
-    const size_t q_base = ((size_t)row * heads + head) * head_dim;
-    float local_max = -INFINITY;
-    for (uint32_t key = threadIdx.x; key < kv_rows; key += blockDim.x) {
-        const size_t k_base = ((size_t)key * heads + head) * head_dim;
-        float dot = 0.0f;
-        for (uint32_t d = 0; d < head_dim; d++)
-            dot = fmaf(hk_bf2f(q[q_base + d]), hk_bf2f(k[k_base + d]), dot);
-        dot *= scale;
-        scores[key] = dot;
-        local_max = fmaxf(local_max, dot);
-    }
-    /* block max through the sum helper's pattern */
-    local_max = hk_wave_max(local_max);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = local_max;
-    __syncthreads();
-    float maximum = -INFINITY;
-    for (uint32_t w = 0; w < (blockDim.x >> 6); w++)
-        maximum = fmaxf(maximum, scratch[w]);
-    float local_sum = 0.0f;
-    for (uint32_t key = threadIdx.x; key < kv_rows; key += blockDim.x) {
-        float p = expf(scores[key] - maximum);
-        scores[key] = p;
-        local_sum += p;
-    }
-    const float inverse = 1.0f / hk_block_sum(local_sum, scratch);
-    for (uint32_t d = threadIdx.x; d < head_dim; d += blockDim.x) {
-        float sum = 0.0f;
-        for (uint32_t key = 0; key < kv_rows; key++)
-            sum = fmaf(scores[key] * inverse,
-                       hk_bf2f(v[((size_t)key * heads + head) * head_dim + d]),
-                       sum);
-        const size_t out = head_major
-            ? ((size_t)head * q_rows + row) * head_dim + d
-            : q_base + d;
-        o[out] = hk_f2bf(sum);
     }
 }
 
@@ -639,13 +595,8 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
         }
         return 1;
     }
-    if ((size_t)kv_rows * sizeof(float) > 64 * 1024)
-        return hk_fail(gpu, "reference attention supports at most 16384 keys");
-    hipLaunchKernelGGL(hk_attn_reference, dim3(q_rows, heads), dim3(256),
-                       (size_t)(kv_rows ? kv_rows : 1) * sizeof(float),
-                       gpu->stream, q, k, v, o, q_rows, kv_rows, heads,
-                       head_dim, scale, head_major);
-    return 1;
+    return hk_attention_reference(gpu, q, k, v, o, q_rows, kv_rows, heads,
+                                  head_dim, scale, head_major);
 }
 
 extern "C" {

@@ -9,10 +9,12 @@
  *   - 256 (W rows) x 256 (X rows) output tile, K step 64;
  *   - four wave64s in a 2x2 grid, each owning a 128x128 sub-tile held as
  *     4x4 accumulators of v_mfma_f32_32x32x16_bf16 (256 f32 per lane);
- *   - X and W tiles staged through LDS with raw buffer loads (16 B per
- *     lane; rows past M read as zero through the buffer bound), double
- *     buffered: the next K step's global loads are in flight while the
- *     current step's 64 MFMAs per wave run;
+ *   - X and W tiles staged into two LDS stages by direct-to-LDS buffer
+ *     loads (16 B per lane; rows past M read as zero through the buffer
+ *     bound).  Once every wave holds a stage's fragments in registers, the
+ *     loads of the stage after next (K step k+2) go into it, one per two
+ *     MFMAs over that stage's last substep and the next stage's first, so
+ *     each load has over two substeps to land;
  *   - LDS rows are 128 B (64 bf16); 16-byte chunks are XOR-swizzled with the
  *     row index so that the 32 rows a fragment read touches fall on
  *     distinct banks;
