@@ -94,16 +94,40 @@ def class_replay(gpu, dit, blocks, mask, reps=2):
 
 def profile_pass(gpu, dit, blocks):
     """Launch pattern for counter collection: warm-up forward, one forward,
-    one replay of the plain GEMMs, then add_bf16 over 64 Mi elements (reads
+    one replay of the plain GEMMs, two launches of the modulation
+    precompute's skinny GEMM, then add_bf16 over 64 Mi elements (reads
     2 x 128 MiB, writes 128 MiB) whose FETCH_SIZE / WRITE_SIZE readings scale
-    the GEMM's counters to bytes."""
-    dit.run_blocks(0, blocks)
-    dit.run_blocks(0, blocks)
+    the other kernels' counters to bytes."""
     L = gpu.L
+    sep = gpu.new_f32(1)
+
+    def separator():
+        # an F32 fill, launched nowhere else in this pass, marks the
+        # measured forward's first and last dispatch for the summariser
+        gpu.begin()
+        L.h3_gpu_fill_normal_f32(gpu.h, sep, 0, 1, 9, 0.0, 1.0)
+        gpu.submit()
+    dit.run_blocks(0, blocks)
+    separator()
+    dit.run_blocks(0, blocks)
+    separator()
     gpu.begin()
     if not L.h3hip_dit_run_blocks_ops(dit.h, 0, blocks, OPS_GEMM):
         raise RuntimeError(dit.error())
     gpu.submit()
+    # the modulation precompute's skinny projection at its H3 shape (39 time
+    # rows x 2688 -> 3 x 6 x 5376), twice
+    m, k, nn = 39, 2688, 3 * 6 * 5376
+    x, w, y = gpu.new_bf16(m * k), gpu.new_bf16(nn * k), gpu.new_bf16(m * nn)
+    gpu.begin()
+    L.h3_gpu_fill_normal_bf16(gpu.h, x, 0, m * k, 7, 0.0, 1.0)
+    L.h3_gpu_fill_normal_bf16(gpu.h, w, 0, nn * k, 8, 0.0, 0.02)
+    for _ in range(2):
+        gpu.check(L.h3_gpu_linear_bf16(gpu.h, y, x, w, None, m, k, nn),
+                  "skinny linear")
+    gpu.submit()
+    for t in (x, w, y):
+        gpu.free(t)
     n = 64 << 20
     a, b, c = gpu.new_bf16(n), gpu.new_bf16(n), gpu.new_bf16(n)
     gpu.begin()
@@ -337,6 +361,18 @@ def load_traffic(name):
         return None
 
 
+def load_counter(key):
+    """A per-forward counter figure from profiles/mfma_util_wan512.json
+    (written from the rocprofv3 --pmc runs of bench.py --profile-pass), or
+    None when no measurement is on file."""
+    path = os.path.join(ROOT, "profiles", "mfma_util_wan512.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(key)
+    except (OSError, ValueError):
+        return None
+
+
 def cpu_model():
     """The host CPU's model name (/proc/cpuinfo), or None."""
     try:
@@ -508,7 +544,15 @@ def main():
                    "parallelism": "single GPU"},
         "ms_per_block": round(ms_step / blocks, 3),
         "s_per_forward": round(ms_step / 1e3, 4),
-        "mfma_util_pct": round(100 * total_tflops / BF16_PEAK_TFLOPS, 1),
+        # MFMA utilisation by counter (SQ_VALU_MFMA_BUSY_CYCLES over the
+        # forward, profiles/counters_wan512_profile_pass.md), and the rate
+        # against the 2.5 PFLOP/s peak derived from this run's timing
+        "mfma_util_pct": load_counter("forward_mfma_busy_pct"),
+        "mfma_util_pct_source": "rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES / "
+                                "GRBM_GUI_ACTIVE over one forward "
+                                "(profiles/mfma_util_wan512.json)",
+        "mfma_rate_pct_derived": round(100 * total_tflops /
+                                       BF16_PEAK_TFLOPS, 1),
         "wall_ms_per_step": round(wall_ms, 3),
         "kernels": {
             name: dict(

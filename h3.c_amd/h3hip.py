@@ -167,6 +167,8 @@ def lib():
                                               _U32, _U32, _U32]),
         "h3_gpu_fill_normal_bf16": (_I, [_P, _P, _SZ, _SZ, C.c_uint64, _F,
                                          _F]),
+        "h3_gpu_fill_normal_f32": (_I, [_P, _P, _SZ, _SZ, C.c_uint64, _F,
+                                        _F]),
         "h3_hip_op_timing_enable": (_I, [_P, _I]),
         "h3_hip_op_timing_reset": (_I, [_P]),
         "h3_hip_op_timing_read": (_I, [_P, C.c_char_p,
