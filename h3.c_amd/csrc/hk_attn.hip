@@ -47,20 +47,18 @@
 #include <type_traits>
 
 #define HK_HD 128
-#define HK_QG 1               /* 32-query groups per wave */
 #define HK_WAVES 8            /* waves per workgroup (two per SIMD) */
 #define HK_THREADS (HK_WAVES * 64)
-#define HK_QB (HK_WAVES * 32 * HK_QG) /* queries per workgroup */
-#define HK_KPT (64 / (HK_THREADS / 16)) /* staged key rows per thread */
+#define HK_QB (HK_WAVES * 32) /* queries per workgroup */
 #define HK_KT 64              /* keys per tile */
-#define HK_K_BYTES (HK_KT * HK_HD * 2)        /* 16 KiB, 256-B rows */
-#define HK_VT_PITCH 136                        /* bytes per V^T row */
-#define HK_VT_BYTES (HK_HD * HK_VT_PITCH)      /* 17 KiB */
-#define HK_STAGE_BYTES (HK_K_BYTES + HK_VT_BYTES)
-#define HK_ATTN_LDS (2 * HK_STAGE_BYTES)
+#define HK_TILE_BYTES (HK_KT * HK_HD * 2)      /* 16 KiB, 256-B rows */
+#define HK_STAGE_BYTES (2 * HK_TILE_BYTES)     /* K tile, then V tile */
+#define HK_ATTN_LDS (2 * HK_STAGE_BYTES)       /* 64 KiB */
+#define HK_ROPE_HALF 48       /* RoPE pairs (d, d + 48), d < 48 */
 
 typedef int hk_v4i __attribute__((ext_vector_type(4)));
 typedef int hk_v2i __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void hk_lds_void;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t hk_attn_rsrc(
     const void *base, uint32_t bytes) {
@@ -69,9 +67,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t hk_attn_rsrc(
                                              0x00020000);
 }
 
-/* K tile: row = key (256 B), 16 chunks, chunk ^= row & 15 */
+/* K tile: row = key (256 B = 16 chunks of 16 B); logical chunk c of row r
+ * sits at physical chunk c ^ (r & 15), so the 32-key fragment reads (one
+ * chunk of 16 consecutive rows per 16 lanes) hit 16 distinct chunks. */
 __device__ __forceinline__ uint32_t hk_k_swz(uint32_t row, uint32_t chunk) {
     return row * 256u + ((chunk ^ (row & 15u)) << 4);
+}
+
+/* V tile: row-major like K, chunk c of row r at c ^ 4 (r & 3).  The
+ * transposing reads take 4 consecutive rows x 32 B per 16 lanes; the XOR
+ * puts the four rows' 32-byte pieces in four different 64-byte bank
+ * groups. */
+__device__ __forceinline__ uint32_t hk_v_swz(uint32_t row, uint32_t chunk) {
+    return row * 256u + ((chunk ^ ((row & 3u) << 2)) << 4);
 }
 
 struct hk_attn_args {
@@ -90,12 +98,36 @@ struct hk_attn_args {
      * (running max in the exp2 domain, sum) into part_ml[pid][256] */
     uint32_t full_units, pieces;
     float *part_o, *part_ml;
+    /* ROPE: bf16 cos / sin tables [rows][48] of the joint sequence; Q and K
+     * arrive unrotated and are rotated in the kernel */
+    const uint16_t *rope_cos, *rope_sin;
+    uint32_t rope_bytes;
 };
 
-template <bool SPARSE, bool SPLIT>
+/* The reference's RoPE pair rotation (h3_cuda_attention.cu:218-233) on 8
+ * pairs: x' = x c - y s, y' = y c + x s in F32, rounded to bf16. */
+__device__ __forceinline__ void hk_rope8(hk_v4i &x, hk_v4i &y, hk_v4i c,
+                                         hk_v4i s) {
+    float xf[8], yf[8], cf[8], sf[8];
+    hk_unpack8(__builtin_bit_cast(uint4, x), xf);
+    hk_unpack8(__builtin_bit_cast(uint4, y), yf);
+    hk_unpack8(__builtin_bit_cast(uint4, c), cf);
+    hk_unpack8(__builtin_bit_cast(uint4, s), sf);
+    float xo[8], yo[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        xo[e] = __builtin_fmaf(xf[e], cf[e], -(yf[e] * sf[e]));
+        yo[e] = __builtin_fmaf(yf[e], cf[e], xf[e] * sf[e]);
+    }
+    x = __builtin_bit_cast(hk_v4i, hk_pack8(xo));
+    y = __builtin_bit_cast(hk_v4i, hk_pack8(yo));
+}
+
+template <bool SPARSE, bool SPLIT, bool ROPE>
 __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t hk_lds[];
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t col = lane & 31u, half = lane >> 5;
 
     uint32_t pid = blockIdx.x;
@@ -106,87 +138,142 @@ __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
     const uint32_t row_stride = a.heads * HK_HD; /* elements */
 
     const __amdgpu_buffer_rsrc_t qr = hk_attn_rsrc(a.q, a.q_bytes);
-    const __amdgpu_buffer_rsrc_t kr = hk_attn_rsrc(a.k, a.kv_bytes);
-    const __amdgpu_buffer_rsrc_t vr = hk_attn_rsrc(a.v, a.kv_bytes);
+    __amdgpu_buffer_rsrc_t cr, sr;
+    if (ROPE) {
+        cr = hk_attn_rsrc(a.rope_cos, a.rope_bytes);
+        sr = hk_attn_rsrc(a.rope_sin, a.rope_bytes);
+    }
 
     /* ---- Q fragments: B operand of S^T = K . Q^T ----
-     * group g, k-step ks: Q[q][16 ks + 8 half .. +8] */
-    const uint32_t qbase = qblock * HK_QB + wave * (32u * HK_QG);
-    hk_bf16x8 qf[HK_QG][8];
-#pragma unroll
-    for (int g = 0; g < HK_QG; g++) {
-        const uint32_t q = qbase + g * 32u + col;
+     * k-step ks: Q[q][16 ks + 8 half .. +8]; with ROPE, dims d < 48 pair
+     * with d + 48, i.e. k-step ks < 3 with ks + 3 in the same lane */
+    const uint32_t qbase = qblock * HK_QB + wave * 32u;
+    hk_bf16x8 qf[8];
+    {
+        const uint32_t q = qbase + col;
         const uint32_t off = q < a.q_rows
             ? ((q * row_stride + head * HK_HD + half * 8u) * 2u)
             : 0xfffffff0u;
+        hk_v4i raw[8];
 #pragma unroll
-        for (int ks = 0; ks < 8; ks++) {
-            hk_v4i raw = __builtin_amdgcn_raw_buffer_load_b128(
+        for (int ks = 0; ks < 8; ks++)
+            raw[ks] = __builtin_amdgcn_raw_buffer_load_b128(
                 qr, off == 0xfffffff0u ? off : off + ks * 32u, 0, 0);
-            qf[g][ks] = __builtin_bit_cast(hk_bf16x8, raw);
+        if (ROPE) {
+            const uint32_t roff = q < a.q_rows
+                ? (q * HK_ROPE_HALF + half * 8u) * 2u : 0xfffffff0u;
+#pragma unroll
+            for (int ks = 0; ks < 3; ks++) {
+                const uint32_t o = roff == 0xfffffff0u ? roff
+                                                       : roff + ks * 32u;
+                hk_v4i c = __builtin_amdgcn_raw_buffer_load_b128(cr, o, 0, 0);
+                hk_v4i s = __builtin_amdgcn_raw_buffer_load_b128(sr, o, 0, 0);
+                hk_rope8(raw[ks], raw[ks + 3], c, s);
+            }
         }
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+            qf[ks] = __builtin_bit_cast(hk_bf16x8, raw[ks]);
     }
 
     /* ---- staging plan ----
-     * K: thread t loads chunk (t & 15) of key rows (t >> 4) + 16 i
-     * V: thread t loads chunk dc = t & 15 of key rows 4 kg .. 4 kg + 3,
-     *    kg = t >> 4, and writes them transposed */
-    const uint32_t sc = tid & 15u, sr = tid >> 4;
-    hk_v4i kreg[HK_KPT], vreg[HK_KPT];
-    auto load_tile = [&](uint32_t kv0) {
+     * V (and K without ROPE) go from global memory straight into LDS with
+     * direct-to-LDS buffer loads: wave w fills rows 8 w .. 8 w + 7 of a
+     * tile in two 1-KiB loads, lane l writing physical chunk l & 15 of row
+     * 4 i + l / 16; the swizzles are applied on the global side.  With
+     * ROPE, K goes through registers instead: thread t owns key row t / 8
+     * and chunk pair t & 7 < 6 ? (t & 7, t & 7 + 6) : (12, 13) / (14, 15),
+     * rotates the pairs and writes the swizzled chunks. */
+    uint32_t k_dma_off[2], v_dma_off[2];
 #pragma unroll
-        for (int i = 0; i < HK_KPT; i++) {
-            const uint32_t krow = kv0 + sr + (HK_THREADS / 16u) * i;
-            const uint32_t koff = krow < a.kv_rows
-                ? ((krow * row_stride + head * HK_HD + sc * 8u) * 2u)
-                : 0xfffffff0u;
-            kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 0, 0);
-            const uint32_t vrow = kv0 + sr * HK_KPT + i;
-            const uint32_t voff = vrow < a.kv_rows
-                ? ((vrow * row_stride + head * HK_HD + sc * 8u) * 2u)
-                : 0xfffffff0u;
-            vreg[i] = __builtin_amdgcn_raw_buffer_load_b128(vr, voff, 0, 0);
+    for (int i = 0; i < 2; i++) {
+        const uint32_t row = (wave * 2u + i) * 4u + (lane >> 4);
+        const uint32_t kc = (lane & 15u) ^ (row & 15u);
+        const uint32_t vc = (lane & 15u) ^ ((row & 3u) << 2);
+        k_dma_off[i] = (row * row_stride + head * HK_HD) * 2u + kc * 16u;
+        v_dma_off[i] = (row * row_stride + head * HK_HD) * 2u + vc * 16u;
+    }
+    const uint32_t kr_row = tid >> 3, kr_part = tid & 7u;
+    const uint32_t kr_c0 = kr_part < 6 ? kr_part : (kr_part == 6 ? 12u : 14u);
+    const uint32_t kr_c1 = kr_part < 6 ? kr_part + 6u : kr_c0 + 1u;
+    hk_v4i kreg[2], kcos, ksin;
+    auto issue_tile = [&](uint32_t kv0, uint32_t stage) {
+        const size_t base = (size_t)kv0 * row_stride;
+        const uint32_t left = a.kv_bytes - kv0 * row_stride * 2u;
+        const __amdgpu_buffer_rsrc_t vr = hk_attn_rsrc(a.v + base, left);
+        uint8_t *st = hk_lds + stage * HK_STAGE_BYTES;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                vr, (hk_lds_void *)(st + HK_TILE_BYTES +
+                                    (wave * 2u + i) * 1024u),
+                16, v_dma_off[i], 0, 0, 0);
+        const __amdgpu_buffer_rsrc_t kr = hk_attn_rsrc(a.k + base, left);
+        if (!ROPE) {
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    kr, (hk_lds_void *)(st + (wave * 2u + i) * 1024u), 16,
+                    k_dma_off[i], 0, 0, 0);
+        } else {
+            const uint32_t ro = (kr_row * row_stride + head * HK_HD) * 2u;
+            kreg[0] = __builtin_amdgcn_raw_buffer_load_b128(
+                kr, ro + kr_c0 * 16u, 0, 0);
+            kreg[1] = __builtin_amdgcn_raw_buffer_load_b128(
+                kr, ro + kr_c1 * 16u, 0, 0);
+            const uint32_t key = kv0 + kr_row;
+            const uint32_t co = key < a.kv_rows && kr_part < 6
+                ? (key * HK_ROPE_HALF + kr_part * 8u) * 2u : 0xfffffff0u;
+            kcos = __builtin_amdgcn_raw_buffer_load_b128(cr, co, 0, 0);
+            ksin = __builtin_amdgcn_raw_buffer_load_b128(sr, co, 0, 0);
         }
     };
-    auto store_tile = [&](uint32_t stage) {
-        uint8_t *ks = hk_lds + stage * HK_STAGE_BYTES;
-        uint8_t *vt = ks + HK_K_BYTES;
-#pragma unroll
-        for (int i = 0; i < HK_KPT; i++)
-            *(hk_v4i *)(ks + hk_k_swz(sr + (HK_THREADS / 16u) * i, sc)) =
-                kreg[i];
-        /* transpose KPT keys x 8 dims -> 8 rows of KPT keys */
-        const uint16_t *v16[HK_KPT];
-#pragma unroll
-        for (int i = 0; i < HK_KPT; i++) v16[i] = (const uint16_t *)&vreg[i];
-#pragma unroll
-        for (int d = 0; d < 8; d++) {
-            uint8_t *dst = vt + (sc * 8u + d) * HK_VT_PITCH + sr * (2u * HK_KPT);
-            if (HK_KPT == 4) {
-                uint2 packed;
-                packed.x = (uint32_t)v16[0][d] | ((uint32_t)v16[1][d] << 16);
-                packed.y = (uint32_t)v16[2][d] | ((uint32_t)v16[3][d] << 16);
-                *(uint2 *)dst = packed;
-            } else {
-                *(uint32_t *)dst =
-                    (uint32_t)v16[0][d] | ((uint32_t)v16[HK_KPT - 1][d] << 16);
-            }
+    /* ROPE: rotate the staged K pairs and write them (after the stage's
+     * previous readers passed the barrier) */
+    auto store_k = [&](uint32_t stage) {
+        if (ROPE) {
+            if (kr_part < 6) hk_rope8(kreg[0], kreg[1], kcos, ksin);
+            uint8_t *st = hk_lds + stage * HK_STAGE_BYTES;
+            *(hk_v4i *)(st + hk_k_swz(kr_row, kr_c0)) = kreg[0];
+            *(hk_v4i *)(st + hk_k_swz(kr_row, kr_c1)) = kreg[1];
         }
     };
 
-    hk_f32x16 o[4][HK_QG];
+    /* fragment addresses (lane parts; the stage and tile sub-block go in
+     * the instructions' offset fields) */
+    const uint32_t lds_base =
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)
+            hk_lds;
+    uint32_t k_frag[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; kk++)
+        k_frag[kk] = lds_base + hk_k_swz(col, kk * 2u + half);
+    /* V^T operand of O^T = V^T . P^T: lane l needs, for dim 32 d + l % 32,
+     * keys 4 half + {0..3} and 8 + 4 half + {0..3} of a 16-key step (the
+     * key order of the P^T operand).  ds_read_b64_tr_b16 hands lane i of a
+     * 16-lane group the column i of a 4-row x 16-column block whose rows
+     * source lanes 4 r .. 4 r + 3 address (4 columns each): source lane
+     * j = l & 15 addresses row 4 half + j / 4, columns 16 (l / 16 & 1) +
+     * 4 (j & 3) of dim block d. */
+    uint32_t v_frag[4];
+    {
+        const uint32_t j = lane & 15u, g1 = (lane >> 4) & 1u;
+        const uint32_t vrow = 4u * half + (j >> 2);
+        const uint32_t low = 2u * g1 + ((j & 3u) >> 1);
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+            const uint32_t chunk = (uint32_t)d * 4u + low;
+            v_frag[d] = lds_base + HK_TILE_BYTES + hk_v_swz(vrow, chunk) +
+                        8u * (j & 1u);
+        }
+    }
+
+    hk_f32x16 o[4];
 #pragma unroll
     for (int d = 0; d < 4; d++)
 #pragma unroll
-        for (int g = 0; g < HK_QG; g++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) o[d][g][r] = 0.0f;
-    float m_run[HK_QG], l_part[HK_QG];
-#pragma unroll
-    for (int g = 0; g < HK_QG; g++) {
-        m_run[g] = -INFINITY;
-        l_part[g] = 0.0f;
-    }
+        for (int r = 0; r < 16; r++) o[d][r] = 0.0f;
+    float m_run = -INFINITY, l_part = 0.0f;
 
     /* ---- key-tile schedule ----
      * Dense: every 64-key tile in order.  Block-sparse: the workgroup's
@@ -202,7 +289,7 @@ __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
     const uint32_t first_tile = SPLIT ? (pid % a.pieces) * piece_tiles : 0;
     const uint32_t dense =
         SPLIT ? min(all_tiles, first_tile + piece_tiles) : all_tiles;
-    uint32_t dense_next = first_tile, ia = 0, ea = 0, ib = 0, eb = 0;
+    uint32_t ia = 0, ea = 0, ib = 0, eb = 0;
     if (SPARSE) {
         const uint32_t qa = qblock * 2u, qb = qa + 1u;
         ia = a.sparse_ptr[qa];
@@ -225,15 +312,9 @@ __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
         }
     }
     const bool first_block = wave < HK_WAVES / 2;
-    /* next tile of the schedule: false when done; in_a / in_b say whose
-     * list holds it */
+    /* next tile of the sparse schedule: false when done; in_a / in_b say
+     * whose list holds it */
     auto advance = [&](uint32_t &tile, bool &in_a, bool &in_b) -> bool {
-        if (!SPARSE) {
-            if (dense_next >= dense) return false;
-            tile = dense_next++;
-            in_a = in_b = true;
-            return true;
-        }
         const uint32_t ta = ia < ea ? a.sparse_idx[ia] : 0xffffffffu;
         const uint32_t tb = ib < eb ? a.sparse_idx[ib] : 0xffffffffu;
         if (ta == 0xffffffffu && tb == 0xffffffffu) return false;
@@ -244,42 +325,33 @@ __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
         if (in_b) ib++;
         return true;
     };
-    uint32_t cur = 0, nxt = 0;
-    bool cur_a = false, cur_b = false, nxt_a = false, nxt_b = false;
-    bool have = advance(cur, cur_a, cur_b);
-    if (have) {
-        load_tile(cur * HK_KT);
-        store_tile(0);
-    }
-    __syncthreads();
 
-    auto tile_step = [&](uint32_t t, uint32_t tile, uint32_t next_tile,
+    /* one tile: MFMAs and softmax on stage STAGE (compile-time, so every
+     * LDS address is a lane register plus an immediate), with the next
+     * tile's loads in flight into the other stage */
+    auto tile_step = [&](auto stage_tag, uint32_t tile, uint32_t next_tile,
                          bool more, bool mine, auto tail_tag) {
+        constexpr uint32_t stage = decltype(stage_tag)::value;
         constexpr bool tail = decltype(tail_tag)::value;
-        const uint32_t stage = t & 1u;
-        if (more) load_tile(next_tile * HK_KT);
-        const uint8_t *ks = hk_lds + stage * HK_STAGE_BYTES;
-        const uint8_t *vt = ks + HK_K_BYTES;
+        if (more) issue_tile(next_tile * HK_KT, stage ^ 1u);
 
         if (mine) {
-        /* S^T[kt][g]: keys kt*32 + .., queries g*32 + col */
-        hk_f32x16 s[2][HK_QG];
+        /* S^T[kt]: keys kt*32 + .., queries col */
+        hk_f32x16 s[2];
 #pragma unroll
         for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-            for (int g = 0; g < HK_QG; g++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) s[kt][g][r] = 0.0f;
+            for (int r = 0; r < 16; r++) s[kt][r] = 0.0f;
 #pragma unroll
         for (int kk = 0; kk < 8; kk++) {
 #pragma unroll
             for (int kt = 0; kt < 2; kt++) {
-                hk_bf16x8 kf = *(const hk_bf16x8 *)(
-                    ks + hk_k_swz(kt * 32u + col, kk * 2u + half));
-#pragma unroll
-                for (int g = 0; g < HK_QG; g++)
-                    s[kt][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                        kf, qf[g][kk], s[kt][g], 0, 0, 0);
+                const hk_bf16x8 kf = *(const hk_bf16x8 *)(
+                    (__attribute__((address_space(3))) uint8_t *)(uintptr_t)
+                        (k_frag[kk] + stage * HK_STAGE_BYTES +
+                         kt * 32u * 256u));
+                s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    kf, qf[kk], s[kt], 0, 0, 0);
             }
         }
 
@@ -293,152 +365,176 @@ __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
          * rounding of P (the bound the tests apply), while l, summed over
          * the unrounded P, is exact up to f32 rounding. */
         const uint32_t kv0 = tile * HK_KT;
-        hk_bf16x8 pf[2][2][HK_QG]; /* [kt][step][g] */
-#pragma unroll
-        for (int g = 0; g < HK_QG; g++) {
-            float mx = -INFINITY;
-            if constexpr (tail) {
-#pragma unroll
-                for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const uint32_t key = kv0 + kt * 32u + (r >> 2) * 8u +
-                                             half * 4u + (r & 3);
-                        if (key >= a.kv_rows) s[kt][g][r] = -INFINITY;
-                    }
-            }
+        hk_bf16x8 pf[2][2]; /* [kt][step] */
+        float mx = -INFINITY;
+        if constexpr (tail) {
 #pragma unroll
             for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-                for (int r = 0; r < 16; r += 2)
-                    mx = __builtin_fmaxf(
-                        mx, __builtin_fmaxf(s[kt][g][r], s[kt][g][r + 1]));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * a.scale_log2;
-            const bool grow = mx > m_run[g] + 8.0f;
-            if (__builtin_amdgcn_ballot_w64(grow)) {
-                const float m_new = fmaxf(m_run[g], mx);
-                const float ref = m_new == -INFINITY ? 0.0f : m_new;
-                const float c = __builtin_amdgcn_exp2f(m_run[g] - ref);
-                m_run[g] = ref;
-                l_part[g] *= c;
-#pragma unroll
-                for (int d = 0; d < 4; d++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) o[d][g][r] *= c;
-            }
-            const float neg = -m_run[g];
-            float sum = 0.0f;
-#pragma unroll
-            for (int kt = 0; kt < 2; kt++) {
-                float p[16];
-#pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    p[r] = __builtin_amdgcn_exp2f(
-                        __builtin_fmaf(s[kt][g][r], a.scale_log2, neg));
-                    sum += p[r];
+                    const uint32_t key = kv0 + kt * 32u + (r >> 2) * 8u +
+                                         half * 4u + (r & 3);
+                    if (key >= a.kv_rows) s[kt][r] = -INFINITY;
                 }
-#pragma unroll
-                for (int st = 0; st < 2; st++) {
-                    hk_bf16x8 v;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) v[e] = (__bf16)p[st * 8 + e];
-                    pf[kt][st][g] = v;
-                }
-            }
-            l_part[g] += sum;
         }
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+            for (int r = 0; r < 16; r += 2)
+                mx = __builtin_fmaxf(
+                    mx, __builtin_fmaxf(s[kt][r], s[kt][r + 1]));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * a.scale_log2;
+        const bool grow = mx > m_run + 8.0f;
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+            const float m_new = fmaxf(m_run, mx);
+            const float ref = m_new == -INFINITY ? 0.0f : m_new;
+            const float c = __builtin_amdgcn_exp2f(m_run - ref);
+            m_run = ref;
+            l_part *= c;
+#pragma unroll
+            for (int d = 0; d < 4; d++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) o[d][r] *= c;
+        }
+        const float neg = -m_run;
+        float sum = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++) {
+            float p[16];
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                p[r] = __builtin_amdgcn_exp2f(
+                    __builtin_fmaf(s[kt][r], a.scale_log2, neg));
+                sum += p[r];
+            }
+#pragma unroll
+            for (int st = 0; st < 2; st++) {
+                hk_bf16x8 v;
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] = (__bf16)p[st * 8 + e];
+                pf[kt][st] = v;
+            }
+        }
+        l_part += sum;
 
-        /* O^T[d][g] += V^T[d, keys] . P^T[keys, g] */
+        /* O^T[d] += V^T[d, keys] . P^T[keys]: the V^T operand comes from
+         * the row-major V tile through two transposing 8-byte reads */
 #pragma unroll
         for (int kt = 0; kt < 2; kt++)
 #pragma unroll
             for (int st = 0; st < 2; st++) {
-                const uint32_t key = kt * 32u + st * 16u + half * 4u;
 #pragma unroll
                 for (int d = 0; d < 4; d++) {
-                    const uint8_t *row = vt + (d * 32u + col) * HK_VT_PITCH;
-                    hk_v2i lo = *(const hk_v2i *)(row + key * 2u);
-                    hk_v2i hi = *(const hk_v2i *)(row + (key + 8u) * 2u);
-                    hk_v4i both = {lo[0], lo[1], hi[0], hi[1]};
-                    hk_bf16x8 vf = __builtin_bit_cast(hk_bf16x8, both);
-#pragma unroll
-                    for (int g = 0; g < HK_QG; g++)
-                        o[d][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                            vf, pf[kt][st][g], o[d][g], 0, 0, 0);
+                    const uint32_t at = v_frag[d] + stage * HK_STAGE_BYTES +
+                                        (kt * 32u + st * 16u) * 256u;
+                    const hk_bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                        (__attribute__((address_space(3))) hk_bf16x4 *)(
+                            uintptr_t)at);
+                    const hk_bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                        (__attribute__((address_space(3))) hk_bf16x4 *)(
+                            uintptr_t)(at + 8u * 256u));
+                    const hk_bf16x8 vf = {lo[0], lo[1], lo[2], lo[3],
+                                          hi[0], hi[1], hi[2], hi[3]};
+                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        vf, pf[kt][st], o[d], 0, 0, 0);
                 }
             }
         } /* mine */
 
-        if (more) store_tile(stage ^ 1u);
+        if (more) store_k(stage ^ 1u);
+        /* the next stage's direct-to-LDS loads (issued by every wave) have
+         * landed once every wave has waited for its own */
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
     };
-    /* the key-range mask is compiled only into the step of the last dense
-     * tile, the only tile with keys past kv_rows */
+
+    using S0 = std::integral_constant<uint32_t, 0>;
+    using S1 = std::integral_constant<uint32_t, 1>;
+    using NT = std::integral_constant<bool, false>;
+    using TT = std::integral_constant<bool, true>;
     if constexpr (!SPARSE) {
-        for (uint32_t t = first_tile; t + 1 < dense; t++)
-            tile_step(t - first_tile, t, t + 1, true, true,
-                      std::integral_constant<bool, false>());
-        tile_step(dense - 1 - first_tile, dense - 1, 0, false, true,
-                  std::integral_constant<bool, true>());
+        /* the key-range mask is compiled only into the step of the last
+         * tile, the only one with keys past kv_rows */
+        const uint32_t n = dense - first_tile;
+        issue_tile(first_tile * HK_KT, 0);
+        store_k(0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        uint32_t i = 0;
+        for (; i + 2 < n; i += 2) {
+            const uint32_t t = first_tile + i;
+            tile_step(S0(), t, t + 1, true, true, NT());
+            tile_step(S1(), t + 1, t + 2, true, true, NT());
+        }
+        if (i + 2 == n) {
+            tile_step(S0(), first_tile + i, first_tile + i + 1, true, true,
+                      NT());
+            tile_step(S1(), first_tile + i + 1, 0, false, true, TT());
+        } else {
+            tile_step(S0(), first_tile + i, 0, false, true, TT());
+        }
     } else {
-        for (uint32_t t = 0; have; t++) {
-            const bool more = advance(nxt, nxt_a, nxt_b);
-            const bool mine = first_block ? cur_a : cur_b;
-            /* one instantiation (register pressure): the key-range mask is
-             * a no-op except on the last dense tile */
-            tile_step(t, cur, nxt, more, mine,
-                      std::integral_constant<bool, true>());
-            cur = nxt;
-            cur_a = nxt_a;
-            cur_b = nxt_b;
-            have = more;
+        uint32_t cur = 0, nxt = 0;
+        bool cur_a = false, cur_b = false, nxt_a = false, nxt_b = false;
+        bool have = advance(cur, cur_a, cur_b);
+        if (have) {
+            issue_tile(cur * HK_KT, 0);
+            store_k(0);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        /* one instantiation per stage (register pressure): the key-range
+         * mask is a no-op except on the last dense tile */
+        while (have) {
+            bool more = advance(nxt, nxt_a, nxt_b);
+            tile_step(S0(), cur, nxt, more, first_block ? cur_a : cur_b,
+                      TT());
+            cur = nxt; cur_a = nxt_a; cur_b = nxt_b; have = more;
+            if (!have) break;
+            more = advance(nxt, nxt_a, nxt_b);
+            tile_step(S1(), cur, nxt, more, first_block ? cur_a : cur_b,
+                      TT());
+            cur = nxt; cur_a = nxt_a; cur_b = nxt_b; have = more;
         }
     }
 
     if constexpr (SPLIT) {
         /* unnormalised partials for the combine kernel */
-#pragma unroll
-        for (int g = 0; g < HK_QG; g++) {
-            const uint32_t ql = wave * (32u * HK_QG) + g * 32u + col;
-            float *po = a.part_o + ((size_t)pid * HK_QB + ql) * HK_HD;
-#pragma unroll
-            for (int d = 0; d < 4; d++)
-#pragma unroll
-                for (int blk = 0; blk < 4; blk++)
-                    *(float4 *)(po + d * 32u + blk * 8u + half * 4u) =
-                        make_float4(o[d][g][blk * 4 + 0], o[d][g][blk * 4 + 1],
-                                    o[d][g][blk * 4 + 2], o[d][g][blk * 4 + 3]);
-            const float l = l_part[g] + __shfl_xor(l_part[g], 32, 64);
-            if (half == 0)
-                *(float2 *)(a.part_ml + ((size_t)pid * HK_QB + ql) * 2u) =
-                    make_float2(m_run[g], l);
-        }
-        return;
-    }
-    /* ---- normalise and store: lane owns query column `col` of group g and
-     * dims d*32 + (r/4)*8 + 4*half + r%4 */
-#pragma unroll
-    for (int g = 0; g < HK_QG; g++) {
-        const float l = l_part[g] + __shfl_xor(l_part[g], 32, 64);
-        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        const uint32_t q = qbase + g * 32u + col;
-        if (q >= a.q_rows) continue;
-        uint16_t *out = a.head_major
-            ? a.o + ((size_t)head * a.q_rows + q) * HK_HD
-            : a.o + (size_t)q * row_stride + (size_t)head * HK_HD;
+        const uint32_t ql = wave * 32u + col;
+        float *po = a.part_o + ((size_t)pid * HK_QB + ql) * HK_HD;
 #pragma unroll
         for (int d = 0; d < 4; d++)
 #pragma unroll
-            for (int blk = 0; blk < 4; blk++) {
-                const uint32_t dim = d * 32u + blk * 8u + half * 4u;
-                uint2 packed = {
-                    hk_pack2(o[d][g][blk * 4 + 0] * inv,
-                             o[d][g][blk * 4 + 1] * inv),
-                    hk_pack2(o[d][g][blk * 4 + 2] * inv,
-                             o[d][g][blk * 4 + 3] * inv)};
-                *(uint2 *)(out + dim) = packed;
-            }
+            for (int blk = 0; blk < 4; blk++)
+                *(float4 *)(po + d * 32u + blk * 8u + half * 4u) =
+                    make_float4(o[d][blk * 4 + 0], o[d][blk * 4 + 1],
+                                o[d][blk * 4 + 2], o[d][blk * 4 + 3]);
+        const float l = l_part + __shfl_xor(l_part, 32, 64);
+        if (half == 0)
+            *(float2 *)(a.part_ml + ((size_t)pid * HK_QB + ql) * 2u) =
+                make_float2(m_run, l);
+        return;
     }
+    /* ---- normalise and store: lane owns query column `col` and dims
+     * d*32 + (r/4)*8 + 4*half + r%4 */
+    const float l = l_part + __shfl_xor(l_part, 32, 64);
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const uint32_t q = qbase + col;
+    if (q >= a.q_rows) return;
+    uint16_t *out = a.head_major
+        ? a.o + ((size_t)head * a.q_rows + q) * HK_HD
+        : a.o + (size_t)q * row_stride + (size_t)head * HK_HD;
+#pragma unroll
+    for (int d = 0; d < 4; d++)
+#pragma unroll
+        for (int blk = 0; blk < 4; blk++) {
+            const uint32_t dim = d * 32u + blk * 8u + half * 4u;
+            uint2 packed = {hk_pack2(o[d][blk * 4 + 0] * inv,
+                                     o[d][blk * 4 + 1] * inv),
+                            hk_pack2(o[d][blk * 4 + 2] * inv,
+                                     o[d][blk * 4 + 3] * inv)};
+            *(uint2 *)(out + dim) = packed;
+        }
 }
 
 /* Combines the key-range pieces of the split work items: per query, with
@@ -483,17 +579,42 @@ __global__ void __launch_bounds__(256) hk_flash_combine(hk_attn_args a) {
 /* devices (bit = ordinal) whose attention kernels have their LDS limit
  * raised */
 static uint64_t hk_attn_lds_ready = 0;
-/* the comma in a template argument list confuses hipLaunchKernelGGL */
-#define HK_FLASH(sparse, split) (hk_flash_fwd<sparse, split>)
+
+template <bool SPARSE, bool SPLIT, bool ROPE>
+static void hk_flash_set_lds() {
+    (void)hipFuncSetAttribute(
+        (const void *)hk_flash_fwd<SPARSE, SPLIT, ROPE>,
+        hipFuncAttributeMaxDynamicSharedMemorySize, HK_ATTN_LDS);
+}
+
+template <bool SPLIT>
+static void hk_flash_launch(struct h3_gpu *gpu, const hk_attn_args &a,
+                            bool masked, bool rope, uint32_t grid) {
+    const dim3 g(grid), b(HK_THREADS);
+    if (masked && rope)
+        hipLaunchKernelGGL((hk_flash_fwd<true, SPLIT, true>), g, b,
+                           HK_ATTN_LDS, gpu->stream, a);
+    else if (masked)
+        hipLaunchKernelGGL((hk_flash_fwd<true, SPLIT, false>), g, b,
+                           HK_ATTN_LDS, gpu->stream, a);
+    else if (rope)
+        hipLaunchKernelGGL((hk_flash_fwd<false, SPLIT, true>), g, b,
+                           HK_ATTN_LDS, gpu->stream, a);
+    else
+        hipLaunchKernelGGL((hk_flash_fwd<false, SPLIT, false>), g, b,
+                           HK_ATTN_LDS, gpu->stream, a);
+}
 
 int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
                       const uint16_t *k, const uint16_t *v, uint16_t *o,
                       uint32_t q_rows, uint32_t kv_rows, uint32_t heads,
                       uint32_t head_dim, float scale, int head_major,
-                      int sparse) {
+                      int sparse, const uint16_t *rope_cos,
+                      const uint16_t *rope_sin) {
     if (!q_rows || !heads) return 1;
     const uint64_t q_bytes = (uint64_t)q_rows * heads * head_dim * 2;
     const uint64_t kv_bytes = (uint64_t)kv_rows * heads * head_dim * 2;
+    const bool rope = rope_cos != NULL;
     /* the reference's debugging knob H3_CUDA_SDPA_NAIVE=1 (read per call,
      * like its backend: h3_cuda_attention.cu) selects the two-pass kernel;
      * H3_HIP_SDPA_NAIVE is the same knob under this backend's prefix */
@@ -505,22 +626,25 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
                        kv_rows > 0 && q_bytes < 0xfffff000ull &&
                        kv_bytes < 0xfffff000ull &&
                        ((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0 &&
-                       ((uintptr_t)v & 15) == 0 && ((uintptr_t)o & 7) == 0;
+                       ((uintptr_t)v & 15) == 0 && ((uintptr_t)o & 7) == 0 &&
+                       (!rope || (((uintptr_t)rope_cos & 15) == 0 &&
+                                  ((uintptr_t)rope_sin & 15) == 0));
+    if (rope && (!flash || q_rows != kv_rows))
+        return hk_fail(gpu, "attention with in-kernel RoPE needs the flash "
+                            "kernel (head_dim 128, 16-byte aligned operands, "
+                            "no reference or naive mode) and q_rows == "
+                            "kv_rows");
     if (flash) {
         const uint64_t lds_bit = 1ull << (gpu->device & 63);
         if (!(hk_attn_lds_ready & lds_bit)) {
-            (void)hipFuncSetAttribute(
-                (const void *)hk_flash_fwd<false, false>,
-                hipFuncAttributeMaxDynamicSharedMemorySize, HK_ATTN_LDS);
-            (void)hipFuncSetAttribute(
-                (const void *)hk_flash_fwd<true, false>,
-                hipFuncAttributeMaxDynamicSharedMemorySize, HK_ATTN_LDS);
-            (void)hipFuncSetAttribute(
-                (const void *)hk_flash_fwd<false, true>,
-                hipFuncAttributeMaxDynamicSharedMemorySize, HK_ATTN_LDS);
-            (void)hipFuncSetAttribute(
-                (const void *)hk_flash_fwd<true, true>,
-                hipFuncAttributeMaxDynamicSharedMemorySize, HK_ATTN_LDS);
+            hk_flash_set_lds<false, false, false>();
+            hk_flash_set_lds<true, false, false>();
+            hk_flash_set_lds<false, true, false>();
+            hk_flash_set_lds<true, true, false>();
+            hk_flash_set_lds<false, false, true>();
+            hk_flash_set_lds<true, false, true>();
+            hk_flash_set_lds<false, true, true>();
+            hk_flash_set_lds<true, true, true>();
             hk_attn_lds_ready |= lds_bit;
         }
         hk_attn_args a;
@@ -536,6 +660,9 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
         a.sparse_ptr = masked ? gpu->sparse_ptr : NULL;
         a.sparse_idx = masked ? gpu->sparse_idx : NULL;
         a.sparse_blocks = (q_rows + 127u) / 128u;
+        a.rope_cos = rope_cos;
+        a.rope_sin = rope_sin;
+        a.rope_bytes = rope ? q_rows * HK_ROPE_HALF * 2u : 0u;
         const uint32_t units = a.q_blocks * heads;
         a.full_units = units;
         a.pieces = 1;
@@ -571,25 +698,10 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
             a.full_units = units - tail;
             a.pieces = pieces;
         }
-        if (a.full_units) {
-            if (masked)
-                hipLaunchKernelGGL(HK_FLASH(true, false), dim3(a.full_units),
-                                   dim3(HK_THREADS), HK_ATTN_LDS, gpu->stream,
-                                   a);
-            else
-                hipLaunchKernelGGL(HK_FLASH(false, false), dim3(a.full_units),
-                                   dim3(HK_THREADS), HK_ATTN_LDS, gpu->stream,
-                                   a);
-        }
+        if (a.full_units)
+            hk_flash_launch<false>(gpu, a, masked, rope, a.full_units);
         if (pieces > 1) {
-            if (masked)
-                hipLaunchKernelGGL(HK_FLASH(true, true), dim3(tail * pieces),
-                                   dim3(HK_THREADS), HK_ATTN_LDS, gpu->stream,
-                                   a);
-            else
-                hipLaunchKernelGGL(HK_FLASH(false, true), dim3(tail * pieces),
-                                   dim3(HK_THREADS), HK_ATTN_LDS, gpu->stream,
-                                   a);
+            hk_flash_launch<true>(gpu, a, masked, rope, tail * pieces);
             hipLaunchKernelGGL(hk_flash_combine, dim3(tail * 32), dim3(256),
                                0, gpu->stream, a);
         }
@@ -618,7 +730,8 @@ static int hk_sdpa(h3_gpu *gpu, h3_gpu_tensor *output,
     hk_op_begin(gpu, name);
     if (!hk_attention_bf16(gpu, HK_CBF16(query), HK_CBF16(key),
                            HK_CBF16(value), HK_BF16(output), q_rows, kv_rows,
-                           heads, head_dim, scale, head_major, sparse))
+                           heads, head_dim, scale, head_major, sparse, NULL,
+                           NULL))
         return 0;
     return hk_op_end(gpu, name, HK_KIND_SDPA);
 }
@@ -639,6 +752,38 @@ int h3_gpu_sdpa_bf16_head_major_output(h3_gpu *gpu, h3_gpu_tensor *output,
                                        uint32_t head_dim, float scale) {
     return hk_sdpa(gpu, output, query, key, value, sequence, sequence, heads,
                    head_dim, scale, 1, 1, "attention");
+}
+
+int h3_hip_sdpa_rope_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                          const h3_gpu_tensor *query,
+                          const h3_gpu_tensor *key,
+                          const h3_gpu_tensor *value,
+                          const h3_gpu_tensor *rope_cos,
+                          const h3_gpu_tensor *rope_sin, uint32_t sequence,
+                          uint32_t heads, uint32_t head_dim,
+                          uint32_t rope_half, float scale) {
+    const size_t count = (size_t)sequence * heads * head_dim;
+    if (!hk_require(gpu, query, count, H3_GPU_BF16, "SDPA query") ||
+        !hk_require(gpu, key, count, H3_GPU_BF16, "SDPA key") ||
+        !hk_require(gpu, value, count, H3_GPU_BF16, "SDPA value") ||
+        !hk_require(gpu, output, count, H3_GPU_BF16, "SDPA output") ||
+        !hk_require(gpu, rope_cos, (size_t)sequence * rope_half, H3_GPU_BF16,
+                    "RoPE cos") ||
+        !hk_require(gpu, rope_sin, (size_t)sequence * rope_half, H3_GPU_BF16,
+                    "RoPE sin") ||
+        !hk_require_active(gpu))
+        return 0;
+    if (rope_half != HK_ROPE_HALF || head_dim != HK_HD)
+        return hk_fail(gpu, "attention with in-kernel RoPE supports head_dim "
+                            "128 with rope_half 48 (got %u / %u)", head_dim,
+                       rope_half);
+    hk_op_begin(gpu, "attention_rope");
+    if (!hk_attention_bf16(gpu, HK_CBF16(query), HK_CBF16(key),
+                           HK_CBF16(value), HK_BF16(output), sequence,
+                           sequence, heads, head_dim, scale, 0, 1,
+                           HK_CBF16(rope_cos), HK_CBF16(rope_sin)))
+        return 0;
+    return hk_op_end(gpu, "attention_rope", HK_KIND_SDPA);
 }
 
 int h3_gpu_sdpa_cross_bf16(h3_gpu *gpu, h3_gpu_tensor *output,

@@ -152,12 +152,15 @@ int hk_gemm_bf16_pair(struct h3_gpu *gpu, const uint16_t *x,
 /* Flash attention; q rows [q_rows][heads][hd], k/v [kv_rows][heads][hd].
  * head_major selects [heads][q_rows][hd] output. */
 /* sparse: apply the registered block-sparse mask (joint attention whose
- * row count matches the registration). */
+ * row count matches the registration).  rope_cos / rope_sin (bf16
+ * [rows][48], self-attention only): Q and K arrive unrotated and the
+ * kernel applies the RoPE pair rotation (d, d + 48), d < 48. */
 int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
                       const uint16_t *k, const uint16_t *v, uint16_t *o,
                       uint32_t q_rows, uint32_t kv_rows, uint32_t heads,
                       uint32_t head_dim, float scale, int head_major,
-                      int sparse);
+                      int sparse, const uint16_t *rope_cos = nullptr,
+                      const uint16_t *rope_sin = nullptr);
 /* The two-pass reference attention (any head size up to 16384 keys). */
 int hk_attention_reference(struct h3_gpu *gpu, const uint16_t *q,
                            const uint16_t *k, const uint16_t *v, uint16_t *o,

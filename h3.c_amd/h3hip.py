@@ -129,6 +129,8 @@ def lib():
         "h3_hip_linear_bf16_noalloc": (_I, [_P, _P, _P, _P, _P, _U32, _U32,
                                             _U32]),
         "h3_hip_device_allocations": (C.c_uint64, [_P]),
+        "h3_hip_sdpa_rope_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _U32, _U32,
+                                       _U32, _U32, _F]),
         "h3_gpu_layer_adaln_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _U32,
                                          _U32, _U32, _U32, _U32, _F]),
         "h3_gpu_gate_layer_adaln_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P,
@@ -270,7 +272,12 @@ def lib():
         "h3hip_euler_velocity_step": (_I, [_P, _P, _SZ, _F, _F]),
     }
     ns = _Prototyped()
+    # H3HIP_ALLOW_MISSING=1 skips entry points an older build lacks (for
+    # timing builds side by side); otherwise a missing one is an error
+    allow_missing = os.environ.get("H3HIP_ALLOW_MISSING") == "1"
     for name, (res, args) in sig.items():
+        if allow_missing and not hasattr(L, name):
+            continue
         fn = getattr(L, name)
         fn.restype = res
         fn.argtypes = args

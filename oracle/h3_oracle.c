@@ -349,6 +349,29 @@ void orc_qkv_rope(const bf16 *qkv, const bf16 *qw, const bf16 *kw,
     }
 }
 
+/* The RoPE pair rotation alone on [rows][heads][hd] bf16 (the rotation
+ * step of h3_cuda_attention.cu:218-233, without the Q/K norm): for
+ * d < half, x'_d = x_d c - x_{d+half} s and x'_{d+half} = x_{d+half} c +
+ * x_d s with c, s = tables[row][d], each as one fused multiply-add over a
+ * rounded product, then bf16; dims from 2 half on are copied. */
+void orc_rope_rotate(const bf16 *in, const bf16 *cosines, const bf16 *sines,
+                     bf16 *out, size_t rows, size_t heads, size_t hd,
+                     size_t half) {
+#pragma omp parallel for schedule(static)
+    for (size_t i = 0; i < rows * heads; i++) {
+        const size_t row = i / heads, b = i * hd;
+        for (size_t d = 0; d < hd; d++) out[b + d] = in[b + d];
+        for (size_t d = 0; d < half && d + half < hd; d++) {
+            const float x = b2f(in[b + d]), y = b2f(in[b + d + half]);
+            const float c = b2f(cosines[row * half + d]);
+            const float s = b2f(sines[row * half + d]);
+            const float ys = y * s, xs = x * s;
+            out[b + d] = f2b(fmaf(x, c, -ys));
+            out[b + d + half] = f2b(fmaf(y, c, xs));
+        }
+    }
+}
+
 /* Non-causal attention, Q [q_rows][heads][hd], K/V [kv_rows][heads][hd].
  * Scores s = scale * sum_d fmaf(q, k) (h3_cuda_attention.cu:505-515);
  * p = exp(s - max).  round_p = 1 applies the flash kernels' rule

@@ -52,6 +52,7 @@ def lib():
             "orc_qkv_rope": [_P, _P, _P, _P, _P, _P, _P, _P, _SZ, _SZ, _SZ,
                              _SZ, _I, _F],
             "orc_sdpa": [_P, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, _F, _I, _I],
+            "orc_rope_rotate": [_P, _P, _P, _P, _SZ, _SZ, _SZ, _SZ],
             "orc_swiglu": [_P, _P, _SZ, _SZ],
             "orc_gelu": [_P, _P, _SZ],
             "orc_silu": [_P, _P, _SZ],
@@ -202,6 +203,15 @@ def qkv_rope(qkv, qw, kw, cos, sin, seq, heads, hd, rope_half, grouped, eps):
                        _p(_u16(cos)), _p(_u16(sin)), _p(q), _p(k), _p(v), seq,
                        heads, hd, rope_half, int(grouped), eps)
     return q, k, v
+
+
+def rope_rotate(x, cos, sin, rows, heads, hd=128, half=48):
+    """The RoPE pair rotation alone (h3_cuda_attention.cu:218-233 without
+    the Q/K norm) on [rows][heads][hd] bf16 bits."""
+    out = np.empty(rows * heads * hd, np.uint16)
+    lib().orc_rope_rotate(_p(_u16(x)), _p(_u16(cos)), _p(_u16(sin)), _p(out),
+                          rows, heads, hd, half)
+    return out
 
 
 def sdpa(q, k, v, q_rows, kv_rows, heads, hd, scale, head_major=False,

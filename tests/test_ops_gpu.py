@@ -420,6 +420,50 @@ def test_sdpa(gpu, q_rows, kv_rows, heads):
                                                  heads, hd, scale))
 
 
+@pytest.mark.parametrize("rows,heads", [
+    (100, 2),       # one query block, ragged single key tile
+    (300, 3),       # two query blocks, ragged tail, key-split pieces
+    (1000, 2),      # 8 key-range pieces per item
+    (2378, 4),      # the H3 length
+])
+def test_sdpa_rope_in_kernel(gpu, rows, heads):
+    """Attention with the RoPE rotation inside the kernel equals the
+    oracle's rotation followed by the oracle's attention."""
+    hd = 128
+    rng = np.random.default_rng(rows * 7 + heads)
+    q, k, v = (rand_bf16(rng, rows * heads * hd) for _ in range(3))
+    ang = rng.uniform(-30, 30, rows * 48)
+    cos, sin = oracle.bf16(np.cos(ang)), oracle.bf16(np.sin(ang))
+    scale = 1.0 / math.sqrt(hd)
+    qr = oracle.rope_rotate(q, cos, sin, rows, heads)
+    kr = oracle.rope_rotate(k, cos, sin, rows, heads)
+    want = oracle.sdpa(qr, kr, v, rows, rows, heads, hd, scale)
+    out = gpu.new_bf16(rows * heads * hd)
+    gpu.run("h3_hip_sdpa_rope_bf16", out, gpu.bf16(q), gpu.bf16(k),
+            gpu.bf16(v), gpu.bf16(cos), gpu.bf16(sin), rows, heads, hd, 48,
+            C.c_float(scale))
+    got = gpu.read_bf16(out)
+    assert_close(got, want, what=f"RoPE SDPA {rows}",
+                 extra_abs=sdpa_p_rounding_bound(qr, kr, v, rows, rows,
+                                                 heads, hd, scale))
+    # and the two-step path through the ordinary kernel
+    ref = gpu.new_bf16(rows * heads * hd)
+    gpu.run("h3_gpu_sdpa_bf16", ref, gpu.bf16(qr), gpu.bf16(kr), gpu.bf16(v),
+            rows, heads, hd, C.c_float(scale))
+    np.testing.assert_array_equal(got, gpu.read_bf16(ref))
+
+
+def test_sdpa_rope_rejects_other_tables(gpu):
+    rows, heads, hd = 64, 1, 128
+    t = gpu.new_bf16(rows * heads * hd)
+    c = gpu.new_bf16(rows * 32)
+    gpu.begin()
+    ok = gpu.L.h3_hip_sdpa_rope_bf16(gpu.h, t, t, t, t, c, c, rows, heads,
+                                     hd, 32, C.c_float(0.1))
+    gpu.submit()
+    assert not ok and "rope_half 48" in gpu.error()
+
+
 @pytest.mark.parametrize("n", [150, 1000])   # 1000: key-split pieces
 def test_sdpa_head_major(gpu, n):
     heads, hd = 2, 128

@@ -564,6 +564,40 @@ def test_h3_blocks_fused_adaln_takes_the_next_blocks_weights():
     assert (np.abs(f64(got).reshape(rows, d) - wrong) > tol).any()
 
 
+def test_rope_rotate_pins():
+    """RoPE rotation alone (h3_cuda_attention.cu:218-233): angle 0 is the
+    identity, angle pi/2 maps (x, y) to (-y, x) exactly, dims from 96 on are
+    copied, the pair norm is kept to bf16 rounding, and on rows whose
+    per-head RMS is exactly 1 with unit norm weights it equals the rotation
+    step of oracle.qkv_rope."""
+    rows, heads, hd = 6, 2, 128
+    x = b(rng.standard_normal(rows * heads * hd))
+    one, zero = b(np.ones(rows * 48)), b(np.zeros(rows * 48))
+    np.testing.assert_array_equal(
+        oracle.rope_rotate(x, one, zero, rows, heads), x)
+    r = f64(oracle.rope_rotate(x, zero, one, rows, heads)).reshape(
+        rows, heads, hd)
+    xf = f64(x).reshape(rows, heads, hd)
+    np.testing.assert_array_equal(r[..., :48], -xf[..., 48:96])
+    np.testing.assert_array_equal(r[..., 48:96], xf[..., :48])
+    np.testing.assert_array_equal(r[..., 96:], xf[..., 96:])
+    ang = rng.uniform(-7, 7, rows * 48)
+    c, s = b(np.cos(ang)), b(np.sin(ang))
+    r = f64(oracle.rope_rotate(x, c, s, rows, heads)).reshape(rows, heads, hd)
+    n0 = xf[..., :48] ** 2 + xf[..., 48:96] ** 2
+    n1 = r[..., :48] ** 2 + r[..., 48:96] ** 2
+    cs = (f64(c) ** 2 + f64(s) ** 2).reshape(rows, 1, 48)
+    assert np.allclose(n1, n0 * cs, rtol=2 ** -6, atol=1e-6)
+    # rows of +-1 have RMS exactly 1, so qkv_rope's norm is the identity
+    sign = b(np.where(rng.standard_normal(rows * heads * hd) < 0, -1.0, 1.0))
+    qkv = np.concatenate([sign.reshape(rows, heads * hd)] * 3,
+                         axis=1).ravel()
+    qn, _, _ = oracle.qkv_rope(qkv, b(np.ones(hd)), b(np.ones(hd)), c, s,
+                               rows, heads, hd, 48, False, 0.0)
+    np.testing.assert_array_equal(
+        oracle.rope_rotate(sign, c, s, rows, heads), qn)
+
+
 def test_bf16_rounding_is_rne():
     """RNE ties: 1 + 2^-8 is halfway between 1 and 1 + 2^-7 -> even (1);
     1 + 3 * 2^-8 -> 1 + 2^-6 (even mantissa)."""
