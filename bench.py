@@ -240,17 +240,23 @@ def h3_measure(gpu, blocks, reps, latent_h=32, latent_w=32, full=True):
 
 def attention_sweep(gpu):
     """flash attention alone, bf16, 40 heads x 128, Q/K/V
-    ~ N(0, 1); self-attention at 6144 and 9720 rows, cross-attention of
-    those queries against 512 keys.  HIP events around 10 launches."""
+    ~ N(0, 1).  Self-attention at 6144 rows (6 x 32 x 32) and 9720 rows
+    (6 x 30 x 54) with the 3D RoPE of those grids applied inside the kernel
+    (h3_hip_sdpa_rope_bf16: Q rotated as it is loaded, K as each tile is
+    staged), and the same attention on pre-rotated Q/K without it
+    (h3_gpu_sdpa_bf16, the kernel the blocks use after their Q/K norm +
+    RoPE pass); cross-attention of those queries against 512 keys.  HIP
+    events around 10 launches each."""
     import ctypes as C
     L = gpu.L
     out = {}
-    scale = 128 ** -0.5
-    for name, q_rows, kv_rows in (("self_6144", 6144, 6144),
-                                  ("self_9720", 9720, 9720),
-                                  ("cross_6144x512", 6144, 512),
-                                  ("cross_9720x512", 9720, 512)):
-        heads = 40
+    scale = C.c_float(128 ** -0.5)
+    heads = 40
+    cases = (("self_6144", 6144, 6144, (6, 32, 32)),
+             ("self_9720", 9720, 9720, (6, 30, 54)),
+             ("cross_6144x512", 6144, 512, None),
+             ("cross_9720x512", 9720, 512, None))
+    for name, q_rows, kv_rows, grid in cases:
         tq = gpu.new_bf16(q_rows * heads * 128)
         tk = gpu.new_bf16(kv_rows * heads * 128)
         tv = gpu.new_bf16(kv_rows * heads * 128)
@@ -260,25 +266,45 @@ def attention_sweep(gpu):
             L.h3_gpu_fill_normal_bf16(gpu.h, t, 0,
                                       L.h3_gpu_tensor_elements(t), 40 + i,
                                       0.0, 1.0)
-        for _ in range(2):
-            L.h3_gpu_sdpa_cross_bf16(gpu.h, to, tq, tk, tv, q_rows, kv_rows,
-                                     heads, 128, scale)
-        L.h3_hip_marker(gpu.h, 6)
-        reps = 10
-        for _ in range(reps):
-            if not L.h3_gpu_sdpa_cross_bf16(gpu.h, to, tq, tk, tv, q_rows,
-                                            kv_rows, heads, 128, scale):
-                raise RuntimeError(gpu.error())
-        L.h3_hip_marker(gpu.h, 7)
         gpu.submit()
-        ms = C.c_double()
-        L.h3_hip_marker_elapsed(gpu.h, 6, 7, C.byref(ms))
-        t = ms.value / reps
-        tf = 4.0 * q_rows * kv_rows * heads * 128 / (t / 1e3) / 1e12
-        out[name] = {"us": round(t * 1e3, 1), "tflops": round(tf, 1),
-                     "frac_of_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
-        for t_ in (tq, tk, tv, to):
-            gpu.free(t_)
+        tc = ts = None
+        if grid:
+            cos, sin = rope_tables(wan_positions(*grid))
+            tc, ts = gpu.bf16(cos), gpu.bf16(sin)
+        variants = ((name, "rope"), (name + "_no_rope", "plain")) if grid \
+            else ((name, "cross"),)
+        for label, mode in variants:
+            def launch():
+                if mode == "rope":
+                    return L.h3_hip_sdpa_rope_bf16(gpu.h, to, tq, tk, tv, tc,
+                                                   ts, q_rows, heads, 128, 48,
+                                                   scale)
+                if mode == "plain":
+                    return L.h3_gpu_sdpa_bf16(gpu.h, to, tq, tk, tv, q_rows,
+                                              heads, 128, scale)
+                return L.h3_gpu_sdpa_cross_bf16(gpu.h, to, tq, tk, tv, q_rows,
+                                                kv_rows, heads, 128, scale)
+            gpu.begin()
+            for _ in range(2):
+                launch()
+            L.h3_hip_marker(gpu.h, 6)
+            reps = 10
+            for _ in range(reps):
+                if not launch():
+                    raise RuntimeError(gpu.error())
+            L.h3_hip_marker(gpu.h, 7)
+            gpu.submit()
+            ms = C.c_double()
+            L.h3_hip_marker_elapsed(gpu.h, 6, 7, C.byref(ms))
+            t = ms.value / reps
+            tf = 4.0 * q_rows * kv_rows * heads * 128 / (t / 1e3) / 1e12
+            out[label] = {"us": round(t * 1e3, 1), "tflops": round(tf, 1),
+                          "frac_of_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+            if mode == "rope":
+                out[label]["rope"] = "3D RoPE in-kernel"
+        for t_ in (tq, tk, tv, to, tc, ts):
+            if t_ is not None:
+                gpu.free(t_)
     return out
 
 

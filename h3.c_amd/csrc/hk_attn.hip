@@ -98,29 +98,59 @@ struct hk_attn_args {
      * (running max in the exp2 domain, sum) into part_ml[pid][256] */
     uint32_t full_units, pieces;
     float *part_o, *part_ml;
-    /* ROPE: bf16 cos / sin tables [rows][48] of the joint sequence; Q and K
-     * arrive unrotated and are rotated in the kernel */
-    const uint16_t *rope_cos, *rope_sin;
+    /* ROPE: the joint sequence's cos / sin tables packed per (row, dim) as
+     * the two bf16 pairs (c, -s), (s, c) of the rotation ([rows][48]
+     * uint64, hk_rope_pack); Q and K arrive unrotated and are rotated in
+     * the kernel */
+    const uint64_t *rope_pk;
     uint32_t rope_bytes;
 };
 
 /* The reference's RoPE pair rotation (h3_cuda_attention.cu:218-233) on 8
- * pairs: x' = x c - y s, y' = y c + x s in F32, rounded to bf16. */
-__device__ __forceinline__ void hk_rope8(hk_v4i &x, hk_v4i &y, hk_v4i c,
-                                         hk_v4i s) {
-    float xf[8], yf[8], cf[8], sf[8];
-    hk_unpack8(__builtin_bit_cast(uint4, x), xf);
-    hk_unpack8(__builtin_bit_cast(uint4, y), yf);
-    hk_unpack8(__builtin_bit_cast(uint4, c), cf);
-    hk_unpack8(__builtin_bit_cast(uint4, s), sf);
+ * pairs, x' = x c - y s and y' = y c + x s, rounded to bf16.  With bf16
+ * inputs both products are exact in F32, so one two-term dot product
+ * (v_dot2_f32_bf16, (x, y) . (c, -s) and (x, y) . (s, c)) rounds exactly
+ * once, as the reference's fma over a rounded (exact) product does.
+ * t[0..3] hold the packed table entries of the 8 dims, two per 16 bytes:
+ * dword 0 / 2 = (c, -s), dword 1 / 3 = (s, c). */
+__device__ __forceinline__ void hk_rope8(hk_v4i &x, hk_v4i &y,
+                                         const hk_v4i t[4]) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
     float xo[8], yo[8];
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        xo[e] = __builtin_fmaf(xf[e], cf[e], -(yf[e] * sf[e]));
-        yo[e] = __builtin_fmaf(yf[e], cf[e], xf[e] * sf[e]);
+    for (int w = 0; w < 4; w++) {
+        const uint32_t xw = (uint32_t)x[w], yw = (uint32_t)y[w];
+        /* (x_2w, y_2w) and (x_2w+1, y_2w+1) */
+        const uint32_t a0 = __builtin_amdgcn_perm(yw, xw, 0x05040100u);
+        const uint32_t a1 = __builtin_amdgcn_perm(yw, xw, 0x07060302u);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t av = h ? a1 : a0;
+            const hk_v4i tv = t[w];
+            const uint32_t b1 = (uint32_t)tv[2 * h], b2 = (uint32_t)tv[2 * h + 1];
+            xo[2 * w + h] = __builtin_amdgcn_fdot2_f32_bf16(
+                __builtin_bit_cast(bf2, av), __builtin_bit_cast(bf2, b1),
+                0.0f, false);
+            yo[2 * w + h] = __builtin_amdgcn_fdot2_f32_bf16(
+                __builtin_bit_cast(bf2, av), __builtin_bit_cast(bf2, b2),
+                0.0f, false);
+        }
     }
     x = __builtin_bit_cast(hk_v4i, hk_pack8(xo));
     y = __builtin_bit_cast(hk_v4i, hk_pack8(yo));
+}
+
+/* Packs bf16 cos / sin tables [rows][48] into the (c, -s), (s, c) pairs
+ * the in-kernel rotation takes. */
+__global__ void __launch_bounds__(256)
+hk_rope_pack(const uint16_t *cosines, const uint16_t *sines, uint64_t *out,
+             uint32_t count) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= count) return;
+    const uint32_t c = cosines[i], sn = sines[i];
+    const uint32_t cs = c | ((sn ^ 0x8000u) << 16);
+    const uint32_t sc = sn | (c << 16);
+    out[i] = (uint64_t)cs | ((uint64_t)sc << 32);
 }
 
 template <bool SPARSE, bool SPLIT, bool ROPE>
@@ -138,11 +168,8 @@ __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
     const uint32_t row_stride = a.heads * HK_HD; /* elements */
 
     const __amdgpu_buffer_rsrc_t qr = hk_attn_rsrc(a.q, a.q_bytes);
-    __amdgpu_buffer_rsrc_t cr, sr;
-    if (ROPE) {
-        cr = hk_attn_rsrc(a.rope_cos, a.rope_bytes);
-        sr = hk_attn_rsrc(a.rope_sin, a.rope_bytes);
-    }
+    __amdgpu_buffer_rsrc_t tr;
+    if (ROPE) tr = hk_attn_rsrc(a.rope_pk, a.rope_bytes);
 
     /* ---- Q fragments: B operand of S^T = K . Q^T ----
      * k-step ks: Q[q][16 ks + 8 half .. +8]; with ROPE, dims d < 48 pair
@@ -160,15 +187,19 @@ __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
             raw[ks] = __builtin_amdgcn_raw_buffer_load_b128(
                 qr, off == 0xfffffff0u ? off : off + ks * 32u, 0, 0);
         if (ROPE) {
+            /* dims 16 ks + 8 half + e, e < 8: 64 bytes of the table */
             const uint32_t roff = q < a.q_rows
-                ? (q * HK_ROPE_HALF + half * 8u) * 2u : 0xfffffff0u;
+                ? (q * HK_ROPE_HALF + half * 8u) * 8u : 0xfffffff0u;
 #pragma unroll
             for (int ks = 0; ks < 3; ks++) {
-                const uint32_t o = roff == 0xfffffff0u ? roff
-                                                       : roff + ks * 32u;
-                hk_v4i c = __builtin_amdgcn_raw_buffer_load_b128(cr, o, 0, 0);
-                hk_v4i s = __builtin_amdgcn_raw_buffer_load_b128(sr, o, 0, 0);
-                hk_rope8(raw[ks], raw[ks + 3], c, s);
+                hk_v4i t[4];
+#pragma unroll
+                for (int p = 0; p < 4; p++)
+                    t[p] = __builtin_amdgcn_raw_buffer_load_b128(
+                        tr, roff == 0xfffffff0u ? roff
+                                                : roff + ks * 128u + p * 16u,
+                        0, 0);
+                hk_rope8(raw[ks], raw[ks + 3], t);
             }
         }
 #pragma unroll
@@ -196,7 +227,7 @@ __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
     const uint32_t kr_row = tid >> 3, kr_part = tid & 7u;
     const uint32_t kr_c0 = kr_part < 6 ? kr_part : (kr_part == 6 ? 12u : 14u);
     const uint32_t kr_c1 = kr_part < 6 ? kr_part + 6u : kr_c0 + 1u;
-    hk_v4i kreg[2], kcos, ksin;
+    hk_v4i kreg[2], ktab[4];
     auto issue_tile = [&](uint32_t kv0, uint32_t stage) {
         const size_t base = (size_t)kv0 * row_stride;
         const uint32_t left = a.kv_bytes - kv0 * row_stride * 2u;
@@ -223,16 +254,18 @@ __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
                 kr, ro + kr_c1 * 16u, 0, 0);
             const uint32_t key = kv0 + kr_row;
             const uint32_t co = key < a.kv_rows && kr_part < 6
-                ? (key * HK_ROPE_HALF + kr_part * 8u) * 2u : 0xfffffff0u;
-            kcos = __builtin_amdgcn_raw_buffer_load_b128(cr, co, 0, 0);
-            ksin = __builtin_amdgcn_raw_buffer_load_b128(sr, co, 0, 0);
+                ? (key * HK_ROPE_HALF + kr_part * 8u) * 8u : 0xfffffff0u;
+#pragma unroll
+            for (int p = 0; p < 4; p++)
+                ktab[p] = __builtin_amdgcn_raw_buffer_load_b128(
+                    tr, co == 0xfffffff0u ? co : co + p * 16u, 0, 0);
         }
     };
     /* ROPE: rotate the staged K pairs and write them (after the stage's
      * previous readers passed the barrier) */
     auto store_k = [&](uint32_t stage) {
         if (ROPE) {
-            if (kr_part < 6) hk_rope8(kreg[0], kreg[1], kcos, ksin);
+            if (kr_part < 6) hk_rope8(kreg[0], kreg[1], ktab);
             uint8_t *st = hk_lds + stage * HK_STAGE_BYTES;
             *(hk_v4i *)(st + hk_k_swz(kr_row, kr_c0)) = kreg[0];
             *(hk_v4i *)(st + hk_k_swz(kr_row, kr_c1)) = kreg[1];
@@ -626,9 +659,7 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
                        kv_rows > 0 && q_bytes < 0xfffff000ull &&
                        kv_bytes < 0xfffff000ull &&
                        ((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0 &&
-                       ((uintptr_t)v & 15) == 0 && ((uintptr_t)o & 7) == 0 &&
-                       (!rope || (((uintptr_t)rope_cos & 15) == 0 &&
-                                  ((uintptr_t)rope_sin & 15) == 0));
+                       ((uintptr_t)v & 15) == 0 && ((uintptr_t)o & 7) == 0;
     if (rope && (!flash || q_rows != kv_rows))
         return hk_fail(gpu, "attention with in-kernel RoPE needs the flash "
                             "kernel (head_dim 128, 16-byte aligned operands, "
@@ -660,9 +691,8 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
         a.sparse_ptr = masked ? gpu->sparse_ptr : NULL;
         a.sparse_idx = masked ? gpu->sparse_idx : NULL;
         a.sparse_blocks = (q_rows + 127u) / 128u;
-        a.rope_cos = rope_cos;
-        a.rope_sin = rope_sin;
-        a.rope_bytes = rope ? q_rows * HK_ROPE_HALF * 2u : 0u;
+        a.rope_pk = NULL;
+        a.rope_bytes = rope ? q_rows * HK_ROPE_HALF * 8u : 0u;
         const uint32_t units = a.q_blocks * heads;
         a.full_units = units;
         a.pieces = 1;
@@ -685,18 +715,34 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
             }
         }
         if (best > 0.6f) pieces = 1;
+        /* scratch: the packed RoPE table, then the split pieces' partials */
+        const size_t table_bytes = ((size_t)a.rope_bytes + 255) & ~(size_t)255;
+        size_t parts = 0;
         if (pieces > 1) {
             /* every piece non-empty */
             const uint32_t per = (kv_tiles + pieces - 1) / pieces;
             pieces = (kv_tiles + per - 1) / per;
-            const size_t parts = (size_t)tail * pieces;
-            float *buf = (float *)hk_splitk_space(
-                gpu, parts * HK_QB * (HK_HD + 2) * sizeof(float));
+            parts = (size_t)tail * pieces;
+        }
+        const size_t part_bytes = parts * HK_QB * (HK_HD + 2) * sizeof(float);
+        if (table_bytes + part_bytes) {
+            uint8_t *buf = (uint8_t *)hk_splitk_space(gpu,
+                                                      table_bytes + part_bytes);
             if (!buf) return 0;
-            a.part_o = buf;
-            a.part_ml = buf + parts * HK_QB * HK_HD;
-            a.full_units = units - tail;
-            a.pieces = pieces;
+            if (rope) {
+                a.rope_pk = (const uint64_t *)buf;
+                const uint32_t count = q_rows * HK_ROPE_HALF;
+                hipLaunchKernelGGL(hk_rope_pack, dim3((count + 255) / 256),
+                                   dim3(256), 0, gpu->stream, rope_cos,
+                                   rope_sin, (uint64_t *)buf, count);
+            }
+            if (parts) {
+                float *pf = (float *)(buf + table_bytes);
+                a.part_o = pf;
+                a.part_ml = pf + parts * HK_QB * HK_HD;
+                a.full_units = units - tail;
+                a.pieces = pieces;
+            }
         }
         if (a.full_units)
             hk_flash_launch<false>(gpu, a, masked, rope, a.full_units);

@@ -4,7 +4,8 @@ properties where it cannot (the 50-block forwards, the full-size denoise).
 
   config 1  Wan block, 5120 hidden, 6x16x16 = 1536 video + 256 text rows
   config 2  Wan block at 512x512x22f: 6x32x32 = 6144 video + 512 text rows
-  config 3  SDPA, 40 heads x 128: self 6144 / 9720, cross 6144 / 9720 x 512
+  config 3  SDPA, 40 heads x 128: self 6144 / 9720 with the 3D RoPE applied
+            in the kernel, cross 6144 / 9720 x 512
   config 4  Wan block at 864x480x22f: 6x30x54 = 9720 + 512 rows (one block
             against the oracle, the 50-block forward through properties)
   config 5  20-step Euler denoise, velocity reuse 2 (the small layout against
@@ -132,9 +133,13 @@ def _sdpa_bound(q, k, v, q_rows, kv_rows, hd, scale):
     return out
 
 
-@pytest.mark.parametrize("q_rows,kv_rows", [
-    (6144, 6144), (9720, 9720), (6144, 512), (9720, 512)])
-def test_config3_sdpa_full_size(gpu, q_rows, kv_rows):
+@pytest.mark.parametrize("q_rows,kv_rows,grid", [
+    (6144, 6144, (6, 32, 32)), (9720, 9720, (6, 30, 54)), (6144, 512, None),
+    (9720, 512, None)])
+def test_config3_sdpa_full_size(gpu, q_rows, kv_rows, grid):
+    """Self-attention with the grid's 3D RoPE applied in the kernel
+    (h3_hip_sdpa_rope_bf16) against the oracle's rotation then attention;
+    cross-attention (no RoPE) against the oracle's attention."""
     heads, hd = 40, 128
     scale = 1.0 / math.sqrt(hd)
     rng = np.random.default_rng(q_rows + kv_rows)
@@ -143,16 +148,21 @@ def test_config3_sdpa_full_size(gpu, q_rows, kv_rows):
     v = rand_bf16(rng, kv_rows * heads * hd)
     tq, tk, tv = gpu.bf16(q), gpu.bf16(k), gpu.bf16(v)
     to = gpu.new_bf16(q_rows * heads * hd)
+    extra = []
     try:
-        if q_rows == kv_rows:
-            gpu.run("h3_gpu_sdpa_bf16", to, tq, tk, tv, q_rows, heads, hd,
-                    C.c_float(scale))
+        if grid:
+            cos, sin = h3hip.rope_tables(h3hip.wan_positions(*grid))
+            cos, sin = oracle.bf16(cos), oracle.bf16(sin)
+            tc, ts = gpu.bf16(cos), gpu.bf16(sin)
+            extra = [tc, ts]
+            gpu.run("h3_hip_sdpa_rope_bf16", to, tq, tk, tv, tc, ts, q_rows,
+                    heads, hd, 48, C.c_float(scale))
         else:
             gpu.run("h3_gpu_sdpa_cross_bf16", to, tq, tk, tv, q_rows, kv_rows,
                     heads, hd, C.c_float(scale))
         got = gpu.read_bf16(to).reshape(q_rows, heads, hd)
     finally:
-        for t in (tq, tk, tv, to):
+        for t in [tq, tk, tv, to] + extra:
             gpu.free(t)
     q3 = q.reshape(q_rows, heads, hd)
     k3 = k.reshape(kv_rows, heads, hd)
@@ -161,6 +171,9 @@ def test_config3_sdpa_full_size(gpu, q_rows, kv_rows):
         qh = np.ascontiguousarray(q3[:, h])
         kh = np.ascontiguousarray(k3[:, h])
         vh = np.ascontiguousarray(v3[:, h])
+        if grid:
+            qh = oracle.rope_rotate(qh, cos, sin, q_rows, 1)
+            kh = oracle.rope_rotate(kh, cos, sin, kv_rows, 1)
         want = oracle.sdpa(qh, kh, vh, q_rows, kv_rows, 1, hd, scale)
         assert_close(np.ascontiguousarray(got[:, h]).ravel(), want,
                      what=f"SDPA {q_rows}x{kv_rows} head {h}",
