@@ -416,7 +416,15 @@ __global__ void __launch_bounds__(HK_THREADS, 1) hk_flash_fwd(hk_attn_args a) {
             for (int r = 0; r < 16; r += 2)
                 mx = __builtin_fmaxf(
                     mx, __builtin_fmaxf(s[kt][r], s[kt][r + 1]));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * a.scale_log2;
+        /* the column's other 16 keys sit in the lane 32 away: one
+         * v_permlane32_swap (no LDS round trip) hands each half the other's
+         * value */
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(
+                __float_as_uint(mx), __float_as_uint(mx), false, false);
+            mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) *
+                 a.scale_log2;
+        }
         const bool grow = mx > m_run + 8.0f;
         if (__builtin_amdgcn_ballot_w64(grow)) {
             const float m_new = fmaxf(m_run, mx);
