@@ -2,6 +2,8 @@
 
     python h3.c_amd/rocprof_summary.py stats <results.db> [top]
         per-kernel calls / total / average / min / max duration (us)
+    python h3.c_amd/rocprof_summary.py stats_csv <run_kernel_stats.csv> [top]
+        the same from rocprofv3's csv output
     python h3.c_amd/rocprof_summary.py pmc <counter_collection.csv> <kernel-substring>
         per-dispatch average of every counter for the kernels matching the
         substring, and for the calibration kernel (hk_elementwise8<2>, add_bf16)
@@ -39,6 +41,21 @@ def stats(db, top=25):
     for name, n, tot, avg, mn, mx in rows[:top]:
         print(f"{name[:60]:60s} {n:6d} {tot / 1e3:12.1f} {avg / 1e3:10.1f} "
               f"{mn / 1e3:10.1f} {mx / 1e3:10.1f} {100 * tot / total:6.2f}")
+
+
+def stats_csv(path, top=25):
+    """The same table from rocprofv3's run_kernel_stats.csv."""
+    rows = list(csv.DictReader(open(path)))
+    total = sum(float(r["TotalDurationNs"]) for r in rows) or 1.0
+    print(f"{'kernel':60s} {'calls':>6s} {'total_us':>12s} {'avg_us':>10s} "
+          f"{'min_us':>10s} {'max_us':>10s} {'pct':>6s}")
+    for r in rows[:top]:
+        name = _short(r["Name"])
+        tot = float(r["TotalDurationNs"])
+        print(f"{name[:60]:60s} {int(r['Calls']):6d} {tot / 1e3:12.1f} "
+              f"{float(r['AverageNs']) / 1e3:10.1f} "
+              f"{float(r['MinNs']) / 1e3:10.1f} "
+              f"{float(r['MaxNs']) / 1e3:10.1f} {100 * tot / total:6.2f}")
 
 
 def pmc(path, match):
@@ -106,7 +123,7 @@ def _groups(path, value="Counter_Value"):
     out = defaultdict(list)
     for _, name, grid, r in rows:
         role = ""
-        if "hk_flash_fwd<false, false>" in name:
+        if "hk_flash_fwd<false, false" in name:
             i = seen[(name, grid)]
             seen[(name, grid)] += 1
             role = "self" if i % 2 == 0 else "cross"
@@ -186,7 +203,9 @@ def kernels(trace_csv, mfma_csv, fetch_csv, write_csv, calib_elements):
 
 
 if __name__ == "__main__":
-    if sys.argv[1] == "stats":
+    if sys.argv[1] == "stats_csv":
+        stats_csv(sys.argv[2], int(sys.argv[3]) if len(sys.argv) > 3 else 25)
+    elif sys.argv[1] == "stats":
         stats(sys.argv[2], int(sys.argv[3]) if len(sys.argv) > 3 else 25)
     elif sys.argv[1] == "forward":
         import json
