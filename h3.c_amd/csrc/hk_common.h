@@ -11,6 +11,7 @@ typedef __bf16 hk_bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 hk_bf16x2 __attribute__((ext_vector_type(2)));
 typedef float hk_f32x16 __attribute__((ext_vector_type(16)));
 typedef float hk_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t hk_u32x4 __attribute__((ext_vector_type(4)));
 
 /* Exact widening: bf16 bits are the top half of the f32 bits. */
 __device__ __forceinline__ float hk_bf2f(uint32_t bits16) {
