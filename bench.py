@@ -241,9 +241,10 @@ def h3_measure(gpu, blocks, reps, latent_h=32, latent_w=32, full=True):
 def attention_sweep(gpu):
     """flash attention alone, bf16, 40 heads x 128, Q/K/V
     ~ N(0, 1).  Self-attention at 6144 rows (6 x 32 x 32) and 9720 rows
-    (6 x 30 x 54) with the 3D RoPE of those grids applied inside the kernel
-    (h3_hip_sdpa_rope_bf16: Q rotated as it is loaded, K as each tile is
-    staged), and the same attention on pre-rotated Q/K without it
+    (6 x 30 x 54) with the 3D RoPE of those grids applied by the call
+    (h3_hip_sdpa_rope_bf16: Q rotated in the attention kernel as it is
+    loaded, K once per key row by a pre-pass; the time covers both), and the
+    same attention on pre-rotated Q/K without it
     (h3_gpu_sdpa_bf16, the kernel the blocks use after their Q/K norm +
     RoPE pass); cross-attention of those queries against 512 keys.  HIP
     events around 10 launches each."""
@@ -301,7 +302,8 @@ def attention_sweep(gpu):
             out[label] = {"us": round(t * 1e3, 1), "tflops": round(tf, 1),
                           "frac_of_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
             if mode == "rope":
-                out[label]["rope"] = "3D RoPE in-kernel"
+                out[label]["rope"] = ("3D RoPE: Q in the attention kernel, "
+                                      "K by a pre-pass; both timed")
         for t_ in (tq, tk, tv, to, tc, ts):
             if t_ is not None:
                 gpu.free(t_)

@@ -57,7 +57,6 @@
 #define HK_QB (HK_WAVES * 32) /* queries per workgroup */
 #define HK_WG_PER_CU (8 / HK_WAVES) /* workgroups per CU: two waves per SIMD */
 #define HK_DMA (16 / HK_WAVES) /* 1-KiB loads per wave per tile and operand */
-#define HK_KJOBS (512 / HK_THREADS) /* RoPE K chunk pairs per thread per tile */
 #define HK_KT 64              /* keys per tile */
 #define HK_TILE_BYTES (HK_KT * HK_HD * 2)      /* 16 KiB, 256-B rows */
 #define HK_STAGE_BYTES (2 * HK_TILE_BYTES)     /* K tile, then V tile */
@@ -108,8 +107,8 @@ struct hk_attn_args {
     float *part_o, *part_ml;
     /* ROPE: the joint sequence's cos / sin tables packed per (row, dim) as
      * the two bf16 pairs (c, -s), (s, c) of the rotation ([rows][48]
-     * uint64, hk_rope_pack); Q and K arrive unrotated and are rotated in
-     * the kernel */
+     * uint64, hk_rope_pack); Q arrives unrotated and is rotated as the
+     * kernel loads its fragments, K was rotated by hk_rope_keys */
     const uint64_t *rope_pk;
     uint32_t rope_bytes;
 };
@@ -159,6 +158,34 @@ hk_rope_pack(const uint16_t *cosines, const uint16_t *sines, uint64_t *out,
     const uint32_t cs = c | ((sn ^ 0x8000u) << 16);
     const uint32_t sc = sn | (c << 16);
     out[i] = (uint64_t)cs | ((uint64_t)sc << 32);
+}
+
+/* Rotates every key row once: K [rows][heads][128] -> out, the RoPE pairs
+ * (d, d + 48), d < 48, through hk_rope8 and dims 96..127 copied.  Thread
+ * t of a (row, head) handles part t & 7: chunk pair (p, p + 6) for p < 6,
+ * chunks (12, 13) and (14, 15) for parts 6 and 7.  Rotating the keys in the
+ * attention kernel instead repeats it for every query block that reads
+ * them (24 at 6144 rows, 38 at 9720). */
+__global__ void __launch_bounds__(256)
+hk_rope_keys(const uint16_t *k, const uint64_t *table, uint16_t *out,
+             uint32_t rows, uint32_t heads) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t part = i & 7u, rh = i >> 3;
+    if (rh >= rows * heads) return;
+    const uint32_t row = rh / heads;
+    const uint32_t c0 = part < 6 ? part : (part == 6 ? 12u : 14u);
+    const uint32_t c1 = part < 6 ? part + 6u : c0 + 1u;
+    const hk_v4i *src = (const hk_v4i *)(k + (size_t)rh * HK_HD);
+    hk_v4i *dst = (hk_v4i *)(out + (size_t)rh * HK_HD);
+    hk_v4i x = src[c0], y = src[c1];
+    if (part < 6) {
+        const hk_v4i *t =
+            (const hk_v4i *)(table + (size_t)row * HK_ROPE_HALF + part * 8u);
+        const hk_v4i tv[4] = {t[0], t[1], t[2], t[3]};
+        hk_rope8(x, y, tv);
+    }
+    dst[c0] = x;
+    dst[c1] = y;
 }
 
 template <bool SPARSE, bool SPLIT, bool ROPE>
@@ -217,13 +244,11 @@ hk_flash_fwd(hk_attn_args a) {
     }
 
     /* ---- staging plan ----
-     * V (and K without ROPE) go from global memory straight into LDS with
-     * direct-to-LDS buffer loads: wave w fills rows 8 w .. 8 w + 7 of a
-     * tile in two 1-KiB loads, lane l writing physical chunk l & 15 of row
-     * 4 i + l / 16; the swizzles are applied on the global side.  With
-     * ROPE, K goes through registers instead: thread t owns key row t / 8
-     * and chunk pair t & 7 < 6 ? (t & 7, t & 7 + 6) : (12, 13) / (14, 15),
-     * rotates the pairs and writes the swizzled chunks. */
+     * K and V go from global memory straight into LDS with direct-to-LDS
+     * buffer loads: wave w fills rows 8 w .. 8 w + 7 of a tile in two
+     * 1-KiB loads, lane l writing physical chunk l & 15 of row 4 i + l / 16;
+     * the swizzles are applied on the global side.  (With ROPE, K arrives
+     * already rotated by hk_rope_keys.) */
     uint32_t k_dma_off[HK_DMA], v_dma_off[HK_DMA];
 #pragma unroll
     for (int i = 0; i < HK_DMA; i++) {
@@ -233,11 +258,6 @@ hk_flash_fwd(hk_attn_args a) {
         k_dma_off[i] = (row * row_stride + head * HK_HD) * 2u + kc * 16u;
         v_dma_off[i] = (row * row_stride + head * HK_HD) * 2u + vc * 16u;
     }
-    const uint32_t kr_row = tid >> 3, kr_part = tid & 7u;
-    const uint32_t kr_c0 = kr_part < 6 ? kr_part : (kr_part == 6 ? 12u : 14u);
-    const uint32_t kr_c1 = kr_part < 6 ? kr_part + 6u : kr_c0 + 1u;
-    /* job j covers key row kr_row + j * (threads / 8) */
-    hk_v4i kreg[HK_KJOBS][2], ktab[HK_KJOBS][4];
     auto issue_tile = [&](uint32_t kv0, uint32_t stage) {
         const size_t base = (size_t)kv0 * row_stride;
         const uint32_t left = a.kv_bytes - kv0 * row_stride * 2u;
@@ -250,44 +270,11 @@ hk_flash_fwd(hk_attn_args a) {
                                     (wave * HK_DMA + i) * 1024u),
                 16, v_dma_off[i], 0, 0, 0);
         const __amdgpu_buffer_rsrc_t kr = hk_attn_rsrc(a.k + base, left);
-        if (!ROPE) {
 #pragma unroll
-            for (int i = 0; i < HK_DMA; i++)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    kr, (hk_lds_void *)(st + (wave * HK_DMA + i) * 1024u), 16,
-                    k_dma_off[i], 0, 0, 0);
-        } else {
-#pragma unroll
-            for (int j = 0; j < HK_KJOBS; j++) {
-                const uint32_t row = kr_row + j * (HK_THREADS / 8u);
-                const uint32_t ro = (row * row_stride + head * HK_HD) * 2u;
-                kreg[j][0] = __builtin_amdgcn_raw_buffer_load_b128(
-                    kr, ro + kr_c0 * 16u, 0, 0);
-                kreg[j][1] = __builtin_amdgcn_raw_buffer_load_b128(
-                    kr, ro + kr_c1 * 16u, 0, 0);
-                const uint32_t key = kv0 + row;
-                const uint32_t co = key < a.kv_rows && kr_part < 6
-                    ? (key * HK_ROPE_HALF + kr_part * 8u) * 8u : 0xfffffff0u;
-#pragma unroll
-                for (int p = 0; p < 4; p++)
-                    ktab[j][p] = __builtin_amdgcn_raw_buffer_load_b128(
-                        tr, co == 0xfffffff0u ? co : co + p * 16u, 0, 0);
-            }
-        }
-    };
-    /* ROPE: rotate the staged K pairs and write them (after the stage's
-     * previous readers passed the barrier) */
-    auto store_k = [&](uint32_t stage) {
-        if (ROPE) {
-            uint8_t *st = hk_lds + stage * HK_STAGE_BYTES;
-#pragma unroll
-            for (int j = 0; j < HK_KJOBS; j++) {
-                const uint32_t row = kr_row + j * (HK_THREADS / 8u);
-                if (kr_part < 6) hk_rope8(kreg[j][0], kreg[j][1], ktab[j]);
-                *(hk_v4i *)(st + hk_k_swz(row, kr_c0)) = kreg[j][0];
-                *(hk_v4i *)(st + hk_k_swz(row, kr_c1)) = kreg[j][1];
-            }
-        }
+        for (int i = 0; i < HK_DMA; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                kr, (hk_lds_void *)(st + (wave * HK_DMA + i) * 1024u), 16,
+                k_dma_off[i], 0, 0, 0);
     };
 
     /* fragment addresses (lane parts; the stage and tile sub-block go in
@@ -502,7 +489,6 @@ hk_flash_fwd(hk_attn_args a) {
             }
         } /* mine */
 
-        if (more) store_k(stage ^ 1u);
         /* the next stage's direct-to-LDS loads (issued by every wave) have
          * landed once every wave has waited for its own */
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -518,7 +504,6 @@ hk_flash_fwd(hk_attn_args a) {
          * tile, the only one with keys past kv_rows */
         const uint32_t n = dense - first_tile;
         issue_tile(first_tile * HK_KT, 0);
-        store_k(0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         uint32_t i = 0;
@@ -540,8 +525,7 @@ hk_flash_fwd(hk_attn_args a) {
         bool have = advance(cur, cur_a, cur_b);
         if (have) {
             issue_tile(cur * HK_KT, 0);
-            store_k(0);
-        }
+            }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         /* one instantiation per stage (register pressure): the key-range
@@ -744,8 +728,10 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
             }
         }
         if (best > 0.6f) pieces = 1;
-        /* scratch: the packed RoPE table, then the split pieces' partials */
+        /* scratch: the packed RoPE table, the rotated keys, then the split
+         * pieces' partials */
         const size_t table_bytes = ((size_t)a.rope_bytes + 255) & ~(size_t)255;
+        const size_t keys_bytes = rope ? ((kv_bytes + 255) & ~(uint64_t)255) : 0;
         size_t parts = 0;
         if (pieces > 1) {
             /* every piece non-empty */
@@ -754,9 +740,9 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
             parts = (size_t)tail * pieces;
         }
         const size_t part_bytes = parts * HK_QB * (HK_HD + 2) * sizeof(float);
-        if (table_bytes + part_bytes) {
-            uint8_t *buf = (uint8_t *)hk_splitk_space(gpu,
-                                                      table_bytes + part_bytes);
+        if (table_bytes + keys_bytes + part_bytes) {
+            uint8_t *buf = (uint8_t *)hk_splitk_space(
+                gpu, table_bytes + keys_bytes + part_bytes);
             if (!buf) return 0;
             if (rope) {
                 a.rope_pk = (const uint64_t *)buf;
@@ -764,9 +750,16 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
                 hipLaunchKernelGGL(hk_rope_pack, dim3((count + 255) / 256),
                                    dim3(256), 0, gpu->stream, rope_cos,
                                    rope_sin, (uint64_t *)buf, count);
+                uint16_t *keys = (uint16_t *)(buf + table_bytes);
+                const uint32_t threads = kv_rows * heads * 8u;
+                hipLaunchKernelGGL(hk_rope_keys, dim3((threads + 255) / 256),
+                                   dim3(256), 0, gpu->stream, k,
+                                   (const uint64_t *)buf, keys, kv_rows,
+                                   heads);
+                a.k = keys;
             }
             if (parts) {
-                float *pf = (float *)(buf + table_bytes);
+                float *pf = (float *)(buf + table_bytes + keys_bytes);
                 a.part_o = pf;
                 a.part_ml = pf + parts * HK_QB * HK_HD;
                 a.full_units = units - tail;

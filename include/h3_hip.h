@@ -48,13 +48,14 @@ int h3_gpu_sdpa_cross_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
                            uint32_t kv_rows, uint32_t heads,
                            uint32_t head_dim, float scale);
 
-/* Self-attention with the 3D RoPE applied inside the attention kernel: Q
- * and K arrive unrotated ([sequence][heads][head_dim] bf16, already
- * normalised where the model normalises them) and the kernel rotates the
- * pairs (d, d + rope_half), d < rope_half, with the bf16 cos / sin tables
- * [sequence][rope_half] -- Q once as its fragments are loaded, K as each
- * key tile is staged -- before the same online-softmax attention as
- * h3_gpu_sdpa_bf16 (the registered block-sparse mask applies as there).
+/* Self-attention with the 3D RoPE applied by the call: Q and K arrive
+ * unrotated ([sequence][heads][head_dim] bf16, already normalised where the
+ * model normalises them) and the pairs (d, d + rope_half), d < rope_half,
+ * are rotated with the bf16 cos / sin tables [sequence][rope_half] -- Q
+ * inside the attention kernel as its fragments are loaded, K once per key
+ * row by a pre-pass into the context's scratch -- before the same
+ * online-softmax attention as h3_gpu_sdpa_bf16 (the registered block-sparse
+ * mask applies as there).
  * The rotation is the reference's RoPE step (h3_cuda_attention.cu:218-233)
  * rounded to bf16, so the result equals rotating Q and K first and calling
  * h3_gpu_sdpa_bf16.  Needs head_dim 128 and rope_half 48 (the 3 x 16
