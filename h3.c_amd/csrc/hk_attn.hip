@@ -93,7 +93,10 @@ struct hk_attn_args {
     const uint16_t *q, *k, *v;
     uint16_t *o;
     uint32_t q_rows, kv_rows, heads, q_blocks;
-    uint32_t q_bytes, kv_bytes;
+    /* bytes readable from q, k and v; elements from one Q / K / V row to
+     * the next (heads * 128, or 3 heads * 128 when the three are read from
+     * the fused QKV projection output) */
+    uint32_t q_bytes, kv_bytes, v_bytes, in_stride;
     float scale_log2;
     int head_major;
     /* block-sparse mask: CSR over 128-row query blocks of 64-row key tiles
@@ -201,7 +204,7 @@ hk_flash_fwd(hk_attn_args a) {
     if ((nwg & 7u) == 0) pid = (pid & 7u) * (nwg >> 3) + (pid >> 3);
     const uint32_t item = SPLIT ? a.full_units + pid / a.pieces : pid;
     const uint32_t qblock = item % a.q_blocks, head = item / a.q_blocks;
-    const uint32_t row_stride = a.heads * HK_HD; /* elements */
+    const uint32_t row_stride = a.in_stride; /* elements, Q / K / V rows */
 
     const __amdgpu_buffer_rsrc_t qr = hk_attn_rsrc(a.q, a.q_bytes);
     __amdgpu_buffer_rsrc_t tr;
@@ -261,7 +264,8 @@ hk_flash_fwd(hk_attn_args a) {
     auto issue_tile = [&](uint32_t kv0, uint32_t stage) {
         const size_t base = (size_t)kv0 * row_stride;
         const uint32_t left = a.kv_bytes - kv0 * row_stride * 2u;
-        const __amdgpu_buffer_rsrc_t vr = hk_attn_rsrc(a.v + base, left);
+        const __amdgpu_buffer_rsrc_t vr =
+            hk_attn_rsrc(a.v + base, a.v_bytes - kv0 * row_stride * 2u);
         uint8_t *st = hk_lds + stage * HK_STAGE_BYTES;
 #pragma unroll
         for (int i = 0; i < HK_DMA; i++)
@@ -568,7 +572,7 @@ hk_flash_fwd(hk_attn_args a) {
     if (q >= a.q_rows) return;
     uint16_t *out = a.head_major
         ? a.o + ((size_t)head * a.q_rows + q) * HK_HD
-        : a.o + (size_t)q * row_stride + (size_t)head * HK_HD;
+        : a.o + (size_t)q * a.heads * HK_HD + (size_t)head * HK_HD;
 #pragma unroll
     for (int d = 0; d < 4; d++)
 #pragma unroll
@@ -655,10 +659,16 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
                       uint32_t q_rows, uint32_t kv_rows, uint32_t heads,
                       uint32_t head_dim, float scale, int head_major,
                       int sparse, const uint16_t *rope_cos,
-                      const uint16_t *rope_sin) {
+                      const uint16_t *rope_sin, int fused_qkv) {
     if (!q_rows || !heads) return 1;
-    const uint64_t q_bytes = (uint64_t)q_rows * heads * head_dim * 2;
-    const uint64_t kv_bytes = (uint64_t)kv_rows * heads * head_dim * 2;
+    /* fused: q, k, v are the three thirds of each [rows][3][heads][hd] row */
+    const uint64_t inner = (uint64_t)heads * head_dim;
+    const uint64_t in_stride = fused_qkv ? 3 * inner : inner;
+    const uint64_t q_bytes = (uint64_t)q_rows * in_stride * 2;
+    const uint64_t kv_bytes =
+        (uint64_t)kv_rows * in_stride * 2 - (fused_qkv ? inner * 2 : 0);
+    const uint64_t v_bytes =
+        (uint64_t)kv_rows * in_stride * 2 - (fused_qkv ? inner * 4 : 0);
     const bool rope = rope_cos != NULL;
     /* the reference's debugging knob H3_CUDA_SDPA_NAIVE=1 (read per call,
      * like its backend: h3_cuda_attention.cu) selects the two-pass kernel;
@@ -672,6 +682,11 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
                        kv_bytes < 0xfffff000ull &&
                        ((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0 &&
                        ((uintptr_t)v & 15) == 0 && ((uintptr_t)o & 7) == 0;
+    if (fused_qkv && (!flash || rope || q_rows != kv_rows))
+        return hk_fail(gpu, "attention on the fused QKV rows needs the flash "
+                            "kernel (head_dim 128, 16-byte aligned rows, no "
+                            "reference or naive mode), no RoPE tables and "
+                            "q_rows == kv_rows");
     if (rope && (!flash || q_rows != kv_rows))
         return hk_fail(gpu, "attention with in-kernel RoPE needs the flash "
                             "kernel (head_dim 128, 16-byte aligned operands, "
@@ -696,6 +711,8 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
         a.q_blocks = (q_rows + HK_QB - 1) / HK_QB;
         a.q_bytes = (uint32_t)q_bytes;
         a.kv_bytes = (uint32_t)kv_bytes;
+        a.v_bytes = (uint32_t)v_bytes;
+        a.in_stride = (uint32_t)in_stride;
         a.scale_log2 = scale * 1.4426950408889634f;
         a.head_major = head_major;
         const bool masked = sparse && gpu->sparse_ptr &&
@@ -821,6 +838,24 @@ int h3_gpu_sdpa_bf16_head_major_output(h3_gpu *gpu, h3_gpu_tensor *output,
                                        uint32_t head_dim, float scale) {
     return hk_sdpa(gpu, output, query, key, value, sequence, sequence, heads,
                    head_dim, scale, 1, 1, "attention");
+}
+
+int h3_hip_sdpa_qkv_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                         const h3_gpu_tensor *qkv, uint32_t sequence,
+                         uint32_t heads, uint32_t head_dim, float scale) {
+    const size_t count = (size_t)sequence * heads * head_dim;
+    if (!hk_require(gpu, qkv, count * 3, H3_GPU_BF16, "SDPA QKV") ||
+        !hk_require(gpu, output, count, H3_GPU_BF16, "SDPA output") ||
+        !hk_require_active(gpu))
+        return 0;
+    const uint16_t *base = HK_CBF16(qkv);
+    const size_t inner = (size_t)heads * head_dim;
+    hk_op_begin(gpu, "attention");
+    if (!hk_attention_bf16(gpu, base, base + inner, base + 2 * inner,
+                           HK_BF16(output), sequence, sequence, heads,
+                           head_dim, scale, 0, 1, NULL, NULL, 1))
+        return 0;
+    return hk_op_end(gpu, "attention", HK_KIND_SDPA);
 }
 
 int h3_hip_sdpa_rope_bf16(h3_gpu *gpu, h3_gpu_tensor *output,

@@ -571,15 +571,20 @@ __device__ __forceinline__ void hk_pack_store(uint16_t *p, const float v[DPL]) {
     *(typename hk_vec_of<DPL>::type *)p = raw;
 }
 
-template <int DPL>
+/* IN_PLACE: the normalised, rotated Q and K go back over their own
+ * elements of qkv (query must be qkv itself; key and value are unused), and
+ * V stays where it is: attention then reads all three from the fused
+ * buffer (h3_hip_sdpa_qkv_bf16).  Each thread reads its elements before any
+ * thread of its row group writes. */
+template <int DPL, bool IN_PLACE = false>
 __global__ void __launch_bounds__(256)
-hk_qk_norm_rope128v(const uint16_t *__restrict__ qkv,
+hk_qk_norm_rope128v(const uint16_t *qkv,
                     const uint16_t *__restrict__ q_weight,
                     const uint16_t *__restrict__ k_weight,
                     const uint16_t *__restrict__ rope_cos,
                     const uint16_t *__restrict__ rope_sin,
-                    uint16_t *__restrict__ query, uint16_t *__restrict__ key,
-                    uint16_t *__restrict__ value, uint32_t sequence,
+                    uint16_t *query, uint16_t *key,
+                    uint16_t *value, uint32_t sequence,
                     uint32_t heads, uint32_t rope_half, uint32_t grouped,
                     float epsilon) {
     constexpr uint32_t HD = 128, LANES = HD / DPL;
@@ -604,7 +609,8 @@ hk_qk_norm_rope128v(const uint16_t *__restrict__ qkv,
     float q[DPL], k[DPL], qw[DPL], kw[DPL];
     hk_unpack<DPL>(qkv + q_base + d0, q);
     hk_unpack<DPL>(qkv + k_base + d0, k);
-    const vec_t vr = *(const vec_t *)(qkv + v_base + d0);
+    vec_t vr;
+    if (!IN_PLACE) vr = *(const vec_t *)(qkv + v_base + d0);
     hk_unpack<DPL>(q_weight + d0, qw);
     hk_unpack<DPL>(k_weight + d0, kw);
     float q_sum = 0.0f, k_sum = 0.0f;
@@ -662,6 +668,11 @@ hk_qk_norm_rope128v(const uint16_t *__restrict__ qkv,
         }
     }
     const size_t out = ((size_t)row * heads + head) * HD + d0;
+    if (IN_PLACE) {
+        hk_pack_store<DPL>(query + q_base + d0, qo);
+        hk_pack_store<DPL>(query + k_base + d0, ko);
+        return;
+    }
     hk_pack_store<DPL>(query + out, qo);
     hk_pack_store<DPL>(key + out, ko);
     *(vec_t *)(value + out) = vr;
@@ -1735,6 +1746,44 @@ int h3_gpu_grouped_qkv_rope_bf16(h3_gpu *gpu, h3_gpu_tensor *query,
     return hk_qkv_rope(gpu, query, key, value, qkv, q_norm, k_norm, rope_cos,
                        rope_sin, sequence, heads, head_dim, rope_half,
                        epsilon, 1u);
+}
+
+int h3_hip_qk_norm_rope_inplace_bf16(h3_gpu *gpu, h3_gpu_tensor *qkv,
+                                     const h3_gpu_tensor *q_norm,
+                                     const h3_gpu_tensor *k_norm,
+                                     const h3_gpu_tensor *rope_cos,
+                                     const h3_gpu_tensor *rope_sin,
+                                     uint32_t sequence, uint32_t heads,
+                                     uint32_t head_dim, uint32_t rope_half,
+                                     float epsilon) {
+    const size_t count = (size_t)sequence * heads * head_dim;
+    if (!HK_REQ_BF16(qkv, count * 3, "QKV") ||
+        !HK_REQ_BF16(q_norm, head_dim, "Q norm") ||
+        !HK_REQ_BF16(k_norm, head_dim, "K norm") ||
+        !HK_REQ_BF16(rope_cos, (size_t)sequence * rope_half, "RoPE cosine") ||
+        !HK_REQ_BF16(rope_sin, (size_t)sequence * rope_half, "RoPE sine") ||
+        !hk_require_active(gpu))
+        return 0;
+    const uintptr_t bases = (uintptr_t)qkv->data | (uintptr_t)q_norm->data |
+                            (uintptr_t)k_norm->data |
+                            (uintptr_t)rope_cos->data |
+                            (uintptr_t)rope_sin->data;
+    if (head_dim != 128 || rope_half % 8 != 0 || rope_half * 2 > head_dim ||
+        (bases & 15u) != 0)
+        return hk_fail(gpu, "in-place Q/K norm + RoPE needs head_dim 128, "
+                            "rope_half a multiple of 8 and 16-byte aligned "
+                            "tensors (got %u / %u)", head_dim, rope_half);
+    hk_op_begin(gpu, "qk_norm_rope_inplace");
+    const size_t vectors = (size_t)sequence * heads;
+    if (vectors)
+        hipLaunchKernelGGL((hk_qk_norm_rope128v<8, true>),
+                           dim3((unsigned)((vectors + 15) / 16)), dim3(256), 0,
+                           gpu->stream, HK_CBF16(qkv), HK_CBF16(q_norm),
+                           HK_CBF16(k_norm), HK_CBF16(rope_cos),
+                           HK_CBF16(rope_sin), HK_BF16(qkv), (uint16_t *)NULL,
+                           (uint16_t *)NULL, sequence, heads, rope_half, 0u,
+                           epsilon);
+    return hk_op_end(gpu, "qk_norm_rope_inplace", HK_KIND_DIRECT);
 }
 
 int h3_gpu_qkv_rope_f32(h3_gpu *gpu, h3_gpu_tensor *query, h3_gpu_tensor *key,

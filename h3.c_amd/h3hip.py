@@ -131,6 +131,9 @@ def lib():
         "h3_hip_device_allocations": (C.c_uint64, [_P]),
         "h3_hip_sdpa_rope_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _U32, _U32,
                                        _U32, _U32, _F]),
+        "h3_hip_qk_norm_rope_inplace_bf16": (_I, [_P, _P, _P, _P, _P, _P, _U32,
+                                                  _U32, _U32, _U32, _F]),
+        "h3_hip_sdpa_qkv_bf16": (_I, [_P, _P, _P, _U32, _U32, _U32, _F]),
         "h3_gpu_layer_adaln_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _U32,
                                          _U32, _U32, _U32, _U32, _F]),
         "h3_gpu_gate_layer_adaln_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P,

@@ -487,14 +487,13 @@ static int run_wan_block(h3hip_dit *dit, uint32_t index, int fuse_next) {
            DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->qkv, dit->mod_a, w->qkv,
                                           w->qkv_bias, rows, d, 3 * inner),
                   "QKV projection") &&
-           DIT_OP(K_ROWS, h3_gpu_qkv_rope_bf16(
-                           gpu, dit->query, dit->key, dit->value, dit->qkv,
-                           w->q_norm, w->k_norm, dit->rope_cos, dit->rope_sin,
-                           rows, c->heads, c->head_dim, c->rope_half, eps),
-                  "Q/K norm + RoPE") &&
-           DIT_OP(K_ATTN, h3_gpu_sdpa_bf16(gpu, dit->attn, dit->query, dit->key,
-                                        dit->value, rows, c->heads,
-                                        c->head_dim, scale),
+           DIT_OP(K_ROWS, h3_hip_qk_norm_rope_inplace_bf16(
+                           gpu, dit->qkv, w->q_norm, w->k_norm, dit->rope_cos,
+                           dit->rope_sin, rows, c->heads, c->head_dim,
+                           c->rope_half, eps),
+                  "Q/K norm + RoPE (in place)") &&
+           DIT_OP(K_ATTN, h3_hip_sdpa_qkv_bf16(gpu, dit->attn, dit->qkv, rows,
+                                            c->heads, c->head_dim, scale),
                   "self-attention") &&
            DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->proj, dit->attn, w->out,
                                           w->out_bias, rows, inner, d),

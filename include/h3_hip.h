@@ -69,6 +69,33 @@ int h3_hip_sdpa_rope_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
                           uint32_t heads, uint32_t head_dim,
                           uint32_t rope_half, float scale);
 
+/* The QKV projection output [sequence][3][heads][head_dim] (Q, K, V
+ * thirds of each row, h3_gpu_qkv_rope_bf16's non-grouped layout), with Q
+ * and K normalised per head and rotated in place: the arithmetic and
+ * rounding of h3_gpu_qkv_rope_bf16 (the reference's qkv_rope_bf16 op,
+ * h3_cuda_attention.cu:190-245), written over Q and K instead of into
+ * separate tensors, and V left where it is.  Needs head_dim 128, rope_half
+ * a multiple of 8 and 16-byte aligned tensors.  With h3_hip_sdpa_qkv_bf16
+ * it saves the copy of Q, K and V out of the fused rows.  No reference
+ * counterpart; used by this backend's Wan-shaped block. */
+int h3_hip_qk_norm_rope_inplace_bf16(h3_gpu *gpu, h3_gpu_tensor *qkv,
+                                     const h3_gpu_tensor *q_norm,
+                                     const h3_gpu_tensor *k_norm,
+                                     const h3_gpu_tensor *rope_cos,
+                                     const h3_gpu_tensor *rope_sin,
+                                     uint32_t sequence, uint32_t heads,
+                                     uint32_t head_dim, uint32_t rope_half,
+                                     float epsilon);
+
+/* h3_gpu_sdpa_bf16 with Q, K and V read from the fused rows
+ * [sequence][3][heads][head_dim] (as left by
+ * h3_hip_qk_norm_rope_inplace_bf16); same kernel, same result as on the
+ * three separate tensors.  Needs head_dim 128 and 16-byte aligned rows.
+ * No reference counterpart; used by this backend's Wan-shaped block. */
+int h3_hip_sdpa_qkv_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                         const h3_gpu_tensor *qkv, uint32_t sequence,
+                         uint32_t heads, uint32_t head_dim, float scale);
+
 /* LayerNorm adaLN:
  *   n = (x - mean) * rsqrt(var + eps) [* w + b]      (w, b may be NULL)
  *   y = bf16(n * (1 + mod[scale]) + mod[shift])

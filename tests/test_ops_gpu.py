@@ -389,6 +389,54 @@ def test_qkv_rope(gpu, grouped, hd, rope_half):
     assert_ulp(gpu.read_bf16(tv), v, 0, "value copy")
 
 
+@pytest.mark.parametrize("seq,heads", [(45, 3), (300, 2), (2378, 4)])
+def test_qkv_in_place_and_fused_attention(gpu, seq, heads):
+    """The in-place Q/K norm + RoPE leaves, in the fused rows, exactly what
+    h3_gpu_qkv_rope_bf16 writes to separate tensors (V untouched), and
+    attention on the fused rows equals attention on those tensors, bit for
+    bit."""
+    hd, rope_half = 128, 48
+    rng = np.random.default_rng(seq + heads)
+    qkv = rand_bf16(rng, seq * 3 * heads * hd)
+    qw, kw = rand_bf16(rng, hd, 0.1, 1.0), rand_bf16(rng, hd, 0.1, 1.0)
+    ang = rng.uniform(-30, 30, seq * rope_half).astype(np.float32)
+    cos, sin = oracle.bf16(np.cos(ang)), oracle.bf16(np.sin(ang))
+    n = seq * heads * hd
+    tq, tk, tv = gpu.new_bf16(n), gpu.new_bf16(n), gpu.new_bf16(n)
+    tqw, tkw, tc, ts = gpu.bf16(qw), gpu.bf16(kw), gpu.bf16(cos), gpu.bf16(sin)
+    gpu.run("h3_gpu_qkv_rope_bf16", tq, tk, tv, gpu.bf16(qkv), tqw, tkw, tc,
+            ts, seq, heads, hd, rope_half, C.c_float(1e-5))
+    fused = gpu.bf16(qkv)
+    gpu.run("h3_hip_qk_norm_rope_inplace_bf16", fused, tqw, tkw, tc, ts, seq,
+            heads, hd, rope_half, C.c_float(1e-5))
+    rows = gpu.read_bf16(fused).view(np.uint16).reshape(seq, 3, heads * hd)
+    q = gpu.read_bf16(tq).view(np.uint16).reshape(seq, heads * hd)
+    k = gpu.read_bf16(tk).view(np.uint16).reshape(seq, heads * hd)
+    v = qkv.view(np.uint16).reshape(seq, 3, heads * hd)[:, 2]
+    assert np.array_equal(rows[:, 0], q)
+    assert np.array_equal(rows[:, 1], k)
+    assert np.array_equal(rows[:, 2], v)
+    scale = C.c_float(1.0 / math.sqrt(hd))
+    split, joint = gpu.new_bf16(n), gpu.new_bf16(n)
+    gpu.run("h3_gpu_sdpa_bf16", split, tq, tk, tv, seq, heads, hd, scale)
+    gpu.run("h3_hip_sdpa_qkv_bf16", joint, fused, seq, heads, hd, scale)
+    assert np.array_equal(gpu.read_bf16(split).view(np.uint16),
+                          gpu.read_bf16(joint).view(np.uint16))
+
+
+def test_qkv_in_place_rejects_other_shapes(gpu):
+    seq, heads, hd = 8, 2, 64
+    buf = gpu.new_bf16(seq * 3 * heads * hd)
+    w = gpu.new_bf16(hd)
+    tab = gpu.new_bf16(seq * 16)
+    gpu.begin()
+    ok = gpu.L.h3_hip_qk_norm_rope_inplace_bf16(gpu.h, buf, w, w, tab, tab,
+                                                seq, heads, hd, 16,
+                                                C.c_float(1e-5))
+    gpu.submit()
+    assert not ok and "head_dim 128" in gpu.error()
+
+
 # ------------------------------------------------------------ attention
 
 @pytest.mark.parametrize("q_rows,kv_rows,heads", [
