@@ -39,6 +39,7 @@
 #include "hk_internal.h"
 
 #include <pthread.h>
+#include <string.h>
 
 #include <math.h>
 #include <stdlib.h>
@@ -125,6 +126,11 @@ struct hk_gemm_args {
     uint32_t pair_tiles;
     const uint16_t *w1, *bias1;
     uint16_t *c1;
+    /* a group of problems of one shape and one X (the GROUP kernel): tile
+     * t is tile t % group_tiles of problem t / group_tiles, whose W, bias
+     * and C are group[3 p], group[3 p + 1], group[3 p + 2] */
+    uint32_t group_tiles;
+    const uint64_t *group;
 };
 
 /* Tile index -> (tile_m, tile_n): column bands of HK_GROUP_M row tiles, so
@@ -141,7 +147,7 @@ __device__ __forceinline__ void hk_tile_coords(uint32_t tile, uint32_t tiles_m,
     tile_n = in_band / band_rows;
 }
 
-template <int EPI>
+template <int EPI, bool GROUP = false>
 __global__ void __launch_bounds__(HK_GEMM_THREADS, 1)
 __attribute__((amdgpu_waves_per_eu(1, 1)))
 hk_gemm_mfma(hk_gemm_args g) {
@@ -174,6 +180,14 @@ hk_gemm_mfma(hk_gemm_args g) {
     uint32_t pid = item;
     uint32_t k_first = 0, split = 0, part = 0;
     const uint16_t *wsrc = g.w;
+    /* grouped: the problem's bias and C addresses are read again by the
+     * epilogue, so that only the index stays live through the main loop */
+    uint32_t prob = 0;
+    if (GROUP) {
+        prob = pid / g.group_tiles;
+        pid -= prob * g.group_tiles;
+        wsrc = (const uint16_t *)g.group[3 * prob];
+    }
     if (partial) {
         split = pid / g.part_tiles;
         part = pid - split * g.part_tiles;
@@ -396,6 +410,9 @@ hk_gemm_mfma(hk_gemm_args g) {
         }
         return;
     }
+    const uint16_t *bias_p =
+        GROUP ? (const uint16_t *)g.group[3 * prob + 1] : g.bias;
+    uint16_t *c_p = GROUP ? (uint16_t *)g.group[3 * prob + 2] : g.c;
     constexpr uint32_t tile_cols = EPI == HK_EPI_SWIGLU ? 128u : HK_BN;
     constexpr uint32_t pitch = tile_cols * 2u;     /* bytes per LDS row */
     constexpr uint32_t chunks = pitch / 16u;
@@ -407,12 +424,12 @@ hk_gemm_mfma(hk_gemm_args g) {
     hk_v2i bias2[4][4];
     if (EPI != HK_EPI_SWIGLU) {
         const __amdgpu_buffer_rsrc_t br =
-            hk_rsrc(g.bias, g.bias ? g.n * 2u : 0u);
+            hk_rsrc(bias_p, bias_p ? g.n * 2u : 0u);
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                if (g.bias) {
+                if (bias_p) {
                     bias2[i][q] = __builtin_amdgcn_raw_buffer_load_b64(
                         br, (n0 + wn * 128u + i * 32u + q * 8u + sub) * 2u, 0,
                         0);
@@ -497,7 +514,7 @@ hk_gemm_mfma(hk_gemm_args g) {
         for (int u = 0; u < 8; u++) {
             const uint32_t m = m0 + row0 + u * rows_per_pass;
             if (m >= g.m || col >= g.n) continue;
-            uint16_t *dst = g.c + (size_t)m * g.n + col;
+            uint16_t *dst = c_p + (size_t)m * g.n + col;
             if (col + 8u <= g.n)
                 __builtin_nontemporal_store(
                     hk_u32x4{v[u].x, v[u].y, v[u].z, v[u].w},
@@ -800,6 +817,9 @@ static void hk_gemm_lds_setup(const struct h3_gpu *gpu) {
     (void)hipFuncSetAttribute(
         (const void *)hk_gemm_mfma<HK_EPI_PARTIAL_SWIGLU>,
         hipFuncAttributeMaxDynamicSharedMemorySize, HK_GEMM_LDS);
+    (void)hipFuncSetAttribute((const void *)hk_gemm_mfma<HK_EPI_STORE, true>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                              HK_GEMM_LDS);
     hk_gemm_lds_ready |= bit;
 }
 
@@ -840,6 +860,8 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
         g.part_tiles = 0;
         g.tile_count = g.tiles_m * g.tiles_n;
         g.pair_tiles = 0;
+        g.group_tiles = 0;
+        g.group = NULL;
         g.w1 = g.bias1 = NULL;
         g.c1 = NULL;
         const uint32_t cus = gpu->num_cus > 0 ? (uint32_t)gpu->num_cus : 256u;
@@ -986,10 +1008,39 @@ int hk_gemm_bf16_pair(struct h3_gpu *gpu, const uint16_t *x,
     g.tile_count = parts * splits;
     g.pair_tiles = tiles;
     g.w1 = w1; g.bias1 = b1; g.c1 = c1;
+    g.group_tiles = 0;
+    g.group = NULL;
     hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_PARTIAL>, dim3(parts * splits),
                        dim3(HK_GEMM_THREADS), HK_GEMM_LDS, gpu->stream, g);
     hipLaunchKernelGGL(hk_splitk_reduce<HK_EPI_STORE>, dim3(parts * 64),
                        dim3(256), 0, gpu->stream, g, splits);
+    return 1;
+}
+
+/* A group of `count` problems C_p = X . W_p^T + bias_p of one shape and one
+ * X, in one data-parallel launch: the problems' tiles are dealt out like
+ * one GEMM's.  `table` is device memory holding (W, bias, C) device
+ * addresses per problem. */
+static int hk_gemm_bf16_group(struct h3_gpu *gpu, const uint16_t *x,
+                              const uint64_t *table, uint32_t count,
+                              uint32_t m, uint32_t n, uint32_t k) {
+    if (!m || !n || !count) return 1;
+    hk_gemm_lds_setup(gpu);
+    hk_gemm_args g;
+    memset(&g, 0, sizeof(g));
+    g.x = x;
+    g.m = m; g.n = n; g.k = k;
+    g.tiles_m = (m + HK_BM - 1) / HK_BM;
+    g.tiles_n = (n + HK_BN - 1) / HK_BN;
+    g.x_bytes = (uint32_t)((uint64_t)m * k * 2);
+    g.w_bytes = (uint32_t)((uint64_t)n * k * 2);
+    g.group_tiles = g.tiles_m * g.tiles_n;
+    g.group = table;
+    g.tile_count = count * g.group_tiles;
+    const uint32_t cus = gpu->num_cus > 0 ? (uint32_t)gpu->num_cus : 256u;
+    hipLaunchKernelGGL((hk_gemm_mfma<HK_EPI_STORE, true>),
+                       dim3(hk_gemm_grid(g.tile_count, cus)),
+                       dim3(HK_GEMM_THREADS), HK_GEMM_LDS, gpu->stream, g);
     return 1;
 }
 
@@ -1094,6 +1145,104 @@ int h3_hip_linear_bf16_noalloc(h3_gpu *gpu, h3_gpu_tensor *output,
                       HK_NOALLOC_SCRATCH_BYTES))
         return 0;
     return hk_op_end(gpu, "gemm", hk_linear_kind(rows, input_dim, output_dim));
+}
+
+h3_gpu_tensor *h3_hip_linear_group_table(h3_gpu *gpu,
+                                         h3_gpu_tensor *const *outputs,
+                                         const h3_gpu_tensor *const *weights,
+                                         const h3_gpu_tensor *const *biases,
+                                         uint32_t count, uint32_t rows,
+                                         uint32_t input_dim,
+                                         uint32_t output_dim) {
+    if (!gpu) return NULL;
+    if (!count || !outputs || !weights) {
+        hk_fail(gpu, "grouped linear table needs at least one problem");
+        return NULL;
+    }
+    uint64_t *entries = (uint64_t *)calloc((size_t)count * 3, sizeof(uint64_t));
+    if (!entries) {
+        hk_fail(gpu, "out of host memory");
+        return NULL;
+    }
+    for (uint32_t p = 0; p < count; p++) {
+        const h3_gpu_tensor *bias = biases ? biases[p] : NULL;
+        if (!hk_require(gpu, weights[p], (size_t)output_dim * input_dim,
+                        H3_GPU_BF16, "grouped linear weight") ||
+            !hk_require(gpu, outputs[p], (size_t)rows * output_dim,
+                        H3_GPU_BF16, "grouped linear output") ||
+            (bias && !hk_require(gpu, bias, output_dim, H3_GPU_BF16,
+                                 "grouped linear bias"))) {
+            free(entries);
+            return NULL;
+        }
+        /* the MFMA path's alignment and range rules, checked once here
+         * (the input's at each launch) */
+        if (!hk_gemm_mfma_ok(gpu, weights[p]->data, weights[p]->data,
+                             bias ? bias->data : NULL, outputs[p]->data, rows,
+                             output_dim, input_dim, HK_EPI_STORE) &&
+            !gpu->reference_kernels) {
+            free(entries);
+            hk_fail(gpu, "grouped linear problem %u: tensors not aligned for "
+                         "the MFMA kernel, or sizes out of its range", p);
+            return NULL;
+        }
+        entries[3 * p] = (uint64_t)(uintptr_t)weights[p]->data;
+        entries[3 * p + 1] = bias ? (uint64_t)(uintptr_t)bias->data : 0;
+        entries[3 * p + 2] = (uint64_t)(uintptr_t)outputs[p]->data;
+    }
+    h3_gpu_tensor *table = h3_gpu_tensor_from_u32(
+        gpu, (const uint32_t *)entries, (size_t)count * 6);
+    free(entries);
+    return table;
+}
+
+int h3_hip_linear_group_bf16(h3_gpu *gpu, const h3_gpu_tensor *table,
+                             uint32_t first, uint32_t count,
+                             const h3_gpu_tensor *input, uint32_t rows,
+                             uint32_t input_dim, uint32_t output_dim) {
+    if (!hk_require(gpu, table, ((size_t)first + count) * 6, H3_GPU_U32,
+                    "grouped linear table") ||
+        !hk_require(gpu, input, (size_t)rows * input_dim, H3_GPU_BF16,
+                    "grouped linear input") ||
+        !hk_require_active(gpu))
+        return 0;
+    if (!count) return 1;
+    const uint64_t *dev = (const uint64_t *)table->data + (size_t)first * 3;
+    const bool mfma = rows > 64 &&
+                      hk_gemm_mfma_ok(gpu, input->data, input->data, NULL,
+                                      input->data, rows, output_dim,
+                                      input_dim, HK_EPI_STORE);
+    hk_op_begin(gpu, "gemm_group");
+    int ok = 1;
+    if (mfma) {
+        ok = hk_gemm_bf16_group(gpu, HK_CBF16(input), dev, count, rows,
+                                output_dim, input_dim);
+    } else {
+        /* reference kernels (or a shape the MFMA kernel does not take):
+         * the problems one by one, from a host copy of the table */
+        uint64_t *entries =
+            (uint64_t *)calloc((size_t)count * 3, sizeof(uint64_t));
+        if (!entries) return hk_fail(gpu, "out of host memory");
+        hipError_t status = hipMemcpyAsync(
+            entries, dev, (size_t)count * 3 * sizeof(uint64_t),
+            hipMemcpyDeviceToHost, gpu->stream);
+        if (status == hipSuccess) status = hipStreamSynchronize(gpu->stream);
+        if (status != hipSuccess) {
+            free(entries);
+            (void)hipGetLastError();
+            return hk_fail_hip(gpu, "grouped linear table read", status);
+        }
+        for (uint32_t p = 0; p < count && ok; p++)
+            ok = hk_gemm_bf16(gpu, HK_CBF16(input),
+                              (const uint16_t *)(uintptr_t)entries[3 * p],
+                              (const uint16_t *)(uintptr_t)entries[3 * p + 1],
+                              (uint16_t *)(uintptr_t)entries[3 * p + 2], rows,
+                              output_dim, input_dim, HK_EPI_STORE);
+        free(entries);
+    }
+    if (!ok) return 0;
+    return hk_op_end(gpu, "gemm_group",
+                     hk_linear_kind(rows, input_dim, output_dim));
 }
 
 int h3_hip_linear_pair_bf16(h3_gpu *gpu, h3_gpu_tensor *output0,

@@ -134,6 +134,10 @@ def lib():
         "h3_hip_qk_norm_rope_inplace_bf16": (_I, [_P, _P, _P, _P, _P, _P, _U32,
                                                   _U32, _U32, _U32, _F]),
         "h3_hip_sdpa_qkv_bf16": (_I, [_P, _P, _P, _U32, _U32, _U32, _F]),
+        "h3_hip_linear_group_table": (_P, [_P, _P, _P, _P, _U32, _U32, _U32,
+                                           _U32]),
+        "h3_hip_linear_group_bf16": (_I, [_P, _P, _U32, _U32, _P, _U32, _U32,
+                                          _U32]),
         "h3_gpu_layer_adaln_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _U32,
                                          _U32, _U32, _U32, _U32, _F]),
         "h3_gpu_gate_layer_adaln_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P,

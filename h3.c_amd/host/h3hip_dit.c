@@ -16,6 +16,9 @@ typedef struct {
     h3_gpu_tensor *cq, *cq_bias, *ck, *ck_bias, *cv, *cv_bias;
     h3_gpu_tensor *cq_norm, *ck_norm, *co, *co_bias;
     h3_gpu_tensor *modulation;
+    /* Wan: this block's cross-attention K and V of the text, projected for
+     * all blocks at the start of a forward (they depend on the text only) */
+    h3_gpu_tensor *ctx_k, *ctx_v;
 } h3hip_block;
 
 struct h3hip_dit {
@@ -27,6 +30,9 @@ struct h3hip_dit {
     h3_gpu_tensor *hidden, *row_map, *rope_cos, *rope_sin, *context;
     h3_gpu_tensor *mod_a, *mod_b, *qkv, *query, *key, *value, *attn, *proj;
     h3_gpu_tensor *cross_q, *cross_k, *cross_v, *cross_out, *ffn_act;
+    /* Wan: the grouped projection's table, problems (block b's K, V) at
+     * 2 b and 2 b + 1 */
+    h3_gpu_tensor *ctx_table;
     int attention_adaln_ready;
     unsigned op_mask;
     /* H3 sampler */
@@ -171,6 +177,8 @@ h3hip_dit *h3hip_dit_create(h3_gpu *gpu, const h3hip_dit_config *config,
             w->ck_norm = bf16(dit, hd, &ok);
             w->co = bf16(dit, d * inner, &ok);
             w->co_bias = bf16(dit, d, &ok);
+            w->ctx_k = bf16(dit, t * inner, &ok);
+            w->ctx_v = bf16(dit, t * inner, &ok);
             w->fc1 = bf16(dit, f * d, &ok);
             w->fc1_bias = bf16(dit, f, &ok);
             w->fc2 = bf16(dit, d * f, &ok);
@@ -201,6 +209,33 @@ h3hip_dit *h3hip_dit_create(h3_gpu *gpu, const h3hip_dit_config *config,
         dit->cross_out = bf16(dit, n * inner, &ok);
         dit->ffn_act = bf16(dit, n * f, &ok);
     }
+    if (ok && is_wan(dit) && t > 0) {
+        const uint32_t problems = 2 * config->blocks;
+        h3_gpu_tensor **outputs =
+            (h3_gpu_tensor **)calloc(problems, sizeof(*outputs));
+        const h3_gpu_tensor **weights =
+            (const h3_gpu_tensor **)calloc(problems, sizeof(*weights));
+        const h3_gpu_tensor **biases =
+            (const h3_gpu_tensor **)calloc(problems, sizeof(*biases));
+        if (outputs && weights && biases) {
+            for (uint32_t b = 0; b < config->blocks; b++) {
+                h3hip_block *w = &dit->blocks[b];
+                outputs[2 * b] = w->ctx_k;
+                outputs[2 * b + 1] = w->ctx_v;
+                weights[2 * b] = w->ck;
+                weights[2 * b + 1] = w->cv;
+                biases[2 * b] = w->ck_bias;
+                biases[2 * b + 1] = w->cv_bias;
+            }
+            dit->ctx_table = h3_hip_linear_group_table(
+                gpu, outputs, weights, biases, problems, (uint32_t)t,
+                (uint32_t)d, (uint32_t)inner);
+        }
+        free(outputs);
+        free(weights);
+        free(biases);
+        if (!dit->ctx_table) ok = 0;
+    }
     if (!ok) {
         if (error && error_size)
             snprintf(error, error_size, "cannot allocate DiT tensors: %s",
@@ -229,7 +264,8 @@ void h3hip_dit_free(h3hip_dit *dit) {
         dit->hidden, dit->row_map, dit->rope_cos, dit->rope_sin,
         dit->context, dit->mod_a, dit->mod_b, dit->qkv, dit->query,
         dit->key, dit->value, dit->attn, dit->proj, dit->cross_q,
-        dit->cross_k, dit->cross_v, dit->cross_out, dit->ffn_act};
+        dit->cross_k, dit->cross_v, dit->cross_out, dit->ffn_act,
+        dit->ctx_table};
     for (size_t i = 0; i < sizeof(shared) / sizeof(*shared); i++)
         h3_gpu_tensor_free(shared[i]);
     sampler_free(dit);
@@ -286,7 +322,8 @@ h3_gpu_tensor *h3hip_dit_tensor(h3hip_dit *dit, const char *name,
         {"ck", w->ck}, {"ck_bias", w->ck_bias}, {"cv", w->cv},
         {"cv_bias", w->cv_bias}, {"cq_norm", w->cq_norm},
         {"ck_norm", w->ck_norm}, {"co", w->co}, {"co_bias", w->co_bias},
-        {"modulation", w->modulation}};
+        {"modulation", w->modulation}, {"ctx_k", w->ctx_k},
+        {"ctx_v", w->ctx_v}};
     for (size_t i = 0; i < sizeof(table) / sizeof(*table); i++)
         if (!strcmp(name, table[i].name)) return table[i].tensor;
     return NULL;
@@ -510,17 +547,9 @@ static int run_wan_block(h3hip_dit *dit, uint32_t index, int fuse_next) {
                                                  w->cq_norm, rows, c->heads,
                                                  c->head_dim, eps),
                   "cross Q norm") &&
-           DIT_OP(K_CTX, h3_hip_linear_pair_bf16(
-                          gpu, dit->cross_k, dit->cross_v, dit->context,
-                          w->ck, w->ck_bias, w->cv, w->cv_bias, t, d, inner),
-                  "cross K/V projections") &&
-           DIT_OP(K_ROWS, h3_gpu_head_rms_norm_bf16(gpu, dit->cross_k,
-                                                 w->ck_norm, t, c->heads,
-                                                 c->head_dim, eps),
-                  "cross K norm") &&
            DIT_OP(K_ATTN, h3_gpu_sdpa_cross_bf16(gpu, dit->cross_out,
-                                              dit->cross_q, dit->cross_k,
-                                              dit->cross_v, rows, t, c->heads,
+                                              dit->cross_q, w->ctx_k,
+                                              w->ctx_v, rows, t, c->heads,
                                               c->head_dim, scale),
                   "cross-attention") &&
            DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->proj, dit->cross_out,
@@ -595,6 +624,24 @@ int h3hip_dit_run_blocks_ops(h3hip_dit *dit, uint32_t first, uint32_t count,
         return dit_fail(dit, "block range [%u, %u) outside %u blocks", first,
                         first + count, dit->config.blocks);
     dit->attention_adaln_ready = 0;
+    if (is_wan(dit) && count && dit->config.text_rows) {
+        /* every block's cross-attention K and V of the text, in one launch,
+         * then each block's K norm */
+        const h3hip_dit_config *c = &dit->config;
+        const uint32_t t = c->text_rows, inner = c->heads * c->head_dim;
+        if (!DIT_OP(K_CTX, h3_hip_linear_group_bf16(
+                               dit->gpu, dit->ctx_table, 2 * first, 2 * count,
+                               dit->context, t, c->hidden, inner),
+                    "cross K/V projections"))
+            return 0;
+        for (uint32_t b = first; b < first + count; b++)
+            if (!DIT_OP(K_ROWS, h3_gpu_head_rms_norm_bf16(
+                                    dit->gpu, dit->blocks[b].ctx_k,
+                                    dit->blocks[b].ck_norm, t, c->heads,
+                                    c->head_dim, c->epsilon),
+                        "cross K norm"))
+                return 0;
+    }
     for (uint32_t b = first; b < first + count; b++) {
         const int fuse_next = b + 1 < first + count;
         int ok = is_wan(dit) ? run_wan_block(dit, b, fuse_next)

@@ -130,6 +130,29 @@ int h3_gpu_gate_layer_adaln_bf16(
     uint32_t slots, uint32_t gate_slot, uint32_t shift_slot,
     uint32_t scale_slot, float epsilon);
 
+/* A group of projections of one input and one shape, output_p = X .
+ * weight_p^T + bias_p for p < count, as one launch: the table
+ * h3_hip_linear_group_table builds holds the problems' device addresses
+ * (free it with h3_gpu_tensor_free; it stays valid while the tensors
+ * live), and h3_hip_linear_group_bf16 runs problems [first, first + count)
+ * of it on `input`.  Tensors must meet the MFMA kernel's alignment (16-byte
+ * weights, 8-byte outputs and biases), which the table checks.  Each
+ * output is exactly what h3_gpu_linear_bf16 computes with the data-
+ * parallel kernel.  Biases may be NULL (or the array NULL).  No reference
+ * counterpart: the Wan-shaped driver projects the text into every block's
+ * cross-attention K and V with one launch. */
+h3_gpu_tensor *h3_hip_linear_group_table(h3_gpu *gpu,
+                                         h3_gpu_tensor *const *outputs,
+                                         const h3_gpu_tensor *const *weights,
+                                         const h3_gpu_tensor *const *biases,
+                                         uint32_t count, uint32_t rows,
+                                         uint32_t input_dim,
+                                         uint32_t output_dim);
+int h3_hip_linear_group_bf16(h3_gpu *gpu, const h3_gpu_tensor *table,
+                             uint32_t first, uint32_t count,
+                             const h3_gpu_tensor *input, uint32_t rows,
+                             uint32_t input_dim, uint32_t output_dim);
+
 /* Two projections of one input, output0 = X . weight0^T + bias0 and
  * output1 = X . weight1^T + bias1, each exactly as h3_gpu_linear_bf16
  * computes it (f32 accumulation, one bf16 rounding).  Small launches

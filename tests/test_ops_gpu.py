@@ -90,6 +90,56 @@ def test_linear_pair(gpu, m, k, n, bias):
                 None, gpu.bf16(w1), None, m, k, n)
 
 
+@pytest.mark.parametrize("m,k,n,count,first,exact", [
+    (300, 256, 512, 5, 0, True),     # 4 K steps: the single linear is
+                                     # data-parallel too, so bit for bit
+    (512, 5120, 1024, 6, 2, False),  # the Wan text shape (narrower), from
+                                     # problem 2 of the table
+    (77, 512, 640, 3, 1, False),     # ragged M and N
+])
+def test_linear_group(gpu, m, k, n, count, first, exact):
+    """h3_hip_linear_group_bf16 runs problems [first, first + count) of a
+    table in one launch: each output against the oracle, and where
+    h3_gpu_linear_bf16 is also data-parallel, equal to it bit for bit;
+    problems outside the range are left alone."""
+    rng = np.random.default_rng(m + k + n + count)
+    total = first + count
+    x = rand_bf16(rng, m * k)
+    ws = [rand_bf16(rng, n * k, 0.05) for _ in range(total)]
+    bs = [rand_bf16(rng, n, 0.1) if p % 2 == 0 else None for p in range(total)]
+    tx = gpu.bf16(x)
+    tws = [gpu.bf16(w) for w in ws]
+    tbs = [gpu.bf16(b) if b is not None else None for b in bs]
+    tos = [gpu.new_bf16(m * n) for _ in range(total)]
+    for t in tos:
+        gpu.run("h3_gpu_fill_normal_bf16", t, 0, m * n, 9, 0.0, 1.0)
+    before = [gpu.read_bf16(t).view(np.uint16).copy() for t in tos]
+    P = C.c_void_p
+    outs = (P * total)(*[t for t in tos])
+    wts = (P * total)(*[t for t in tws])
+    bis = (P * total)(*[t for t in tbs])
+    table = gpu.L.h3_hip_linear_group_table(gpu.h, outs, wts, bis, total, m,
+                                            k, n)
+    assert table, gpu.error()
+    try:
+        gpu.run("h3_hip_linear_group_bf16", table, first, count, tx, m, k, n)
+        for p in range(total):
+            got = gpu.read_bf16(tos[p])
+            if p < first:
+                assert np.array_equal(got.view(np.uint16), before[p])
+                continue
+            assert_close(got, oracle.linear(x, ws[p], bs[p], m, k, n),
+                         what=f"group[{p}] {m}x{k}x{n}")
+            if exact:
+                one = gpu.new_bf16(m * n)
+                gpu.run("h3_gpu_linear_bf16", one, tx, tws[p], tbs[p], m, k,
+                        n)
+                assert np.array_equal(gpu.read_bf16(one).view(np.uint16),
+                                      got.view(np.uint16))
+    finally:
+        gpu.L.h3_gpu_tensor_free(table)
+
+
 def test_linear_stats_kind(gpu):
     """Routing-shape rule of the stats counters (reference
     h3_cuda_core.cu:838-841): rows >= 32, in >= 256, out >= 256 -> kind 1."""
