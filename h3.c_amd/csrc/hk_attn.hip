@@ -114,6 +114,13 @@ struct hk_attn_args {
      * kernel loads its fragments, K was rotated by hk_rope_keys */
     const uint64_t *rope_pk;
     uint32_t rope_bytes;
+    /* Q_NORM: the per-head RMS norm of Q (weight q_norm[128], epsilon
+     * q_eps) applied as the Q fragments are loaded, then, with q_cos /
+     * q_sin ([rows][48] bf16), the RoPE pairs (d, d + 48) -- the arithmetic
+     * and rounding of hk_head_rms128 / hk_qk_norm_rope128v, so the result
+     * equals normalising (and rotating) Q first */
+    const uint16_t *q_norm, *q_cos, *q_sin;
+    float q_eps;
 };
 
 /* The reference's RoPE pair rotation (h3_cuda_attention.cu:218-233) on 8
@@ -148,6 +155,21 @@ __device__ __forceinline__ void hk_rope8(hk_v4i &x, hk_v4i &y,
     }
     x = __builtin_bit_cast(hk_v4i, hk_pack8(xo));
     y = __builtin_bit_cast(hk_v4i, hk_pack8(yo));
+}
+
+/* Correctly rounded square root of a positive normal float (the inputs
+ * here are at least the norm's epsilon).  This file's fast-math flags turn
+ * sqrtf (and __fsqrt_rn) into the bare v_sqrt_f32, which can be an ulp
+ * off; the row kernels' sqrtf is the IEEE one.  The hardware estimate s is
+ * within an ulp, and the residuals x - s' s of its two neighbours s' pick
+ * the correctly rounded one (the expansion the compiler uses for IEEE
+ * sqrtf). */
+__device__ __forceinline__ float hk_sqrt_rn(float x) {
+    const float s = __builtin_amdgcn_sqrtf(x);
+    const float down = __uint_as_float(__float_as_uint(s) - 1u);
+    const float up = __uint_as_float(__float_as_uint(s) + 1u);
+    float r = __builtin_fmaf(-down, s, x) <= 0.0f ? down : s;
+    return __builtin_fmaf(-up, s, x) > 0.0f ? up : r;
 }
 
 /* Packs bf16 cos / sin tables [rows][48] into the (c, -s), (s, c) pairs
@@ -240,6 +262,94 @@ hk_flash_fwd(hk_attn_args a) {
                         0, 0);
                 hk_rope8(raw[ks], raw[ks + 3], t);
             }
+        }
+        if (a.q_norm) {
+            /* the row kernels' lanes hold dims 8 j .. 8 j + 7, j < 16, and
+             * sum them with a fma chain, then over j with an xor tree
+             * (8, 4, 2, 1); chunk j here is k-step j / 2 of the lane half
+             * j % 2, so the tree's first three levels pair k-steps
+             * (ks, ks + 4), (ks, ks ^ 2), (ks, ks ^ 1) in the lane and the
+             * last pairs the two halves. */
+            float x[8][8], part[8];
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++) {
+                part[ks] = 0.0f;
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    const uint32_t bits = (uint32_t)raw[ks][w];
+                    x[ks][2 * w] = hk_bf2f(bits & 0xffffu);
+                    x[ks][2 * w + 1] = hk_bf2f(bits >> 16);
+                }
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    part[ks] = __builtin_fmaf(x[ks][e], x[ks][e], part[ks]);
+                /* this file's -fassociative-math would otherwise merge the
+                 * partial sums into one chain: each sum is pinned */
+                asm volatile("" : "+v"(part[ks]));
+            }
+            float l1[4];
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                l1[ks] = part[ks] + part[ks + 4];
+                asm volatile("" : "+v"(l1[ks]));
+            }
+            float l2a = l1[0] + l1[2], l2b = l1[1] + l1[3];
+            asm volatile("" : "+v"(l2a), "+v"(l2b));
+            float l3 = l2a + l2b;
+            asm volatile("" : "+v"(l3));
+            const auto sw = __builtin_amdgcn_permlane32_swap(
+                __float_as_uint(l3), __float_as_uint(l3), false, false);
+            /* lanes < 32 find the other half's value in the second
+             * result, lanes >= 32 in the first */
+            const float other = __uint_as_float(half ? sw[0] : sw[1]);
+            float total = l3 + other;
+            asm volatile("" : "+v"(total));
+            const float inv = __fdiv_rn(
+                1.0f, hk_sqrt_rn(__builtin_fmaf(total, 0.0078125f, a.q_eps)));
+            const hk_v4i *wv = (const hk_v4i *)a.q_norm;
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++) {
+                const hk_v4i wr = wv[2 * ks + half];
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    const uint32_t bits = (uint32_t)wr[w];
+                    /* (x inv) w, rounded in that order (pinned, or the
+                     * flags would let it become x (inv w)) */
+                    float lo = x[ks][2 * w] * inv, hi = x[ks][2 * w + 1] * inv;
+                    asm volatile("" : "+v"(lo), "+v"(hi));
+                    x[ks][2 * w] = lo * hk_bf2f(bits & 0xffffu);
+                    x[ks][2 * w + 1] = hi * hk_bf2f(bits >> 16);
+                }
+            }
+            if (a.q_cos) {
+                const bool live = q < a.q_rows;
+                const hk_v4i *cv = (const hk_v4i *)(a.q_cos +
+                    (size_t)(live ? q : 0) * HK_ROPE_HALF + half * 8u);
+                const hk_v4i *sv = (const hk_v4i *)(a.q_sin +
+                    (size_t)(live ? q : 0) * HK_ROPE_HALF + half * 8u);
+#pragma unroll
+                for (int ks = 0; ks < 3; ks++) {
+                    const hk_v4i cr = cv[2 * ks], sr = sv[2 * ks];
+#pragma unroll
+                    for (int w = 0; w < 4; w++) {
+#pragma unroll
+                        for (int h = 0; h < 2; h++) {
+                            const uint32_t cb = (uint32_t)cr[w], sb = (uint32_t)sr[w];
+                            const float c = hk_bf2f(h ? cb >> 16 : cb & 0xffffu);
+                            const float sn = hk_bf2f(h ? sb >> 16 : sb & 0xffffu);
+                            const int e = 2 * w + h;
+                            const float lo = x[ks][e], hi = x[ks + 3][e];
+                            float hs = hi * sn, ls = lo * sn;
+                            asm volatile("" : "+v"(hs), "+v"(ls));
+                            x[ks][e] = __builtin_fmaf(lo, c, -hs);
+                            x[ks + 3][e] = __builtin_fmaf(hi, c, ls);
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++)
+                raw[ks] = __builtin_bit_cast(hk_v4i, hk_pack8(x[ks]));
         }
 #pragma unroll
         for (int ks = 0; ks < 8; ks++)
@@ -659,7 +769,9 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
                       uint32_t q_rows, uint32_t kv_rows, uint32_t heads,
                       uint32_t head_dim, float scale, int head_major,
                       int sparse, const uint16_t *rope_cos,
-                      const uint16_t *rope_sin, int fused_qkv) {
+                      const uint16_t *rope_sin, int fused_qkv,
+                      const uint16_t *q_norm, const uint16_t *q_cos,
+                      const uint16_t *q_sin, float q_eps) {
     if (!q_rows || !heads) return 1;
     /* fused: q, k, v are the three thirds of each [rows][3][heads][hd] row */
     const uint64_t inner = (uint64_t)heads * head_dim;
@@ -682,6 +794,14 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
                        kv_bytes < 0xfffff000ull &&
                        ((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0 &&
                        ((uintptr_t)v & 15) == 0 && ((uintptr_t)o & 7) == 0;
+    if (q_norm && (!flash || rope || ((uintptr_t)q_norm & 15) ||
+                   ((uintptr_t)q_cos & 15) || ((uintptr_t)q_sin & 15) ||
+                   (!q_cos) != (!q_sin)))
+        return hk_fail(gpu, "attention with the Q norm in the kernel needs "
+                            "the flash kernel (head_dim 128, 16-byte aligned "
+                            "operands, no reference or naive mode), "
+                            "16-byte aligned weight and tables, and no "
+                            "in-kernel RoPE of the unnormalised Q");
     if (fused_qkv && (!flash || rope || q_rows != kv_rows))
         return hk_fail(gpu, "attention on the fused QKV rows needs the flash "
                             "kernel (head_dim 128, 16-byte aligned rows, no "
@@ -713,6 +833,10 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
         a.kv_bytes = (uint32_t)kv_bytes;
         a.v_bytes = (uint32_t)v_bytes;
         a.in_stride = (uint32_t)in_stride;
+        a.q_norm = q_norm;
+        a.q_cos = q_cos;
+        a.q_sin = q_sin;
+        a.q_eps = q_eps;
         a.scale_log2 = scale * 1.4426950408889634f;
         a.head_major = head_major;
         const bool masked = sparse && gpu->sparse_ptr &&
@@ -856,6 +980,71 @@ int h3_hip_sdpa_qkv_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
                            head_dim, scale, 0, 1, NULL, NULL, 1))
         return 0;
     return hk_op_end(gpu, "attention", HK_KIND_SDPA);
+}
+
+int h3_hip_sdpa_qkv_norm_rope_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                                   const h3_gpu_tensor *qkv,
+                                   const h3_gpu_tensor *q_norm,
+                                   const h3_gpu_tensor *rope_cos,
+                                   const h3_gpu_tensor *rope_sin,
+                                   uint32_t sequence, uint32_t heads,
+                                   uint32_t head_dim, uint32_t rope_half,
+                                   float epsilon, float scale) {
+    const size_t count = (size_t)sequence * heads * head_dim;
+    if (!hk_require(gpu, qkv, count * 3, H3_GPU_BF16, "SDPA QKV") ||
+        !hk_require(gpu, output, count, H3_GPU_BF16, "SDPA output") ||
+        !hk_require(gpu, q_norm, head_dim, H3_GPU_BF16, "Q norm") ||
+        (rope_cos && !hk_require(gpu, rope_cos, (size_t)sequence * rope_half,
+                                 H3_GPU_BF16, "RoPE cos")) ||
+        (rope_sin && !hk_require(gpu, rope_sin, (size_t)sequence * rope_half,
+                                 H3_GPU_BF16, "RoPE sin")) ||
+        !hk_require_active(gpu))
+        return 0;
+    if (head_dim != HK_HD || (rope_cos && rope_half != HK_ROPE_HALF) ||
+        (!rope_cos) != (!rope_sin))
+        return hk_fail(gpu, "attention with the Q norm in the kernel supports "
+                            "head_dim 128 and RoPE tables of rope_half 48 "
+                            "(got %u / %u)", head_dim, rope_half);
+    const uint16_t *base = HK_CBF16(qkv);
+    const size_t inner = (size_t)heads * head_dim;
+    hk_op_begin(gpu, "attention");
+    if (!hk_attention_bf16(gpu, base, base + inner, base + 2 * inner,
+                           HK_BF16(output), sequence, sequence, heads,
+                           head_dim, scale, 0, 1, NULL, NULL, 1,
+                           HK_CBF16(q_norm),
+                           rope_cos ? HK_CBF16(rope_cos) : NULL,
+                           rope_sin ? HK_CBF16(rope_sin) : NULL, epsilon))
+        return 0;
+    return hk_op_end(gpu, "attention", HK_KIND_SDPA);
+}
+
+int h3_hip_sdpa_cross_norm_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                                const h3_gpu_tensor *query,
+                                const h3_gpu_tensor *key,
+                                const h3_gpu_tensor *value,
+                                const h3_gpu_tensor *q_norm, uint32_t q_rows,
+                                uint32_t kv_rows, uint32_t heads,
+                                uint32_t head_dim, float epsilon,
+                                float scale) {
+    const size_t qc = (size_t)q_rows * heads * head_dim;
+    const size_t kc = (size_t)kv_rows * heads * head_dim;
+    if (!hk_require(gpu, query, qc, H3_GPU_BF16, "SDPA query") ||
+        !hk_require(gpu, key, kc, H3_GPU_BF16, "SDPA key") ||
+        !hk_require(gpu, value, kc, H3_GPU_BF16, "SDPA value") ||
+        !hk_require(gpu, output, qc, H3_GPU_BF16, "SDPA output") ||
+        !hk_require(gpu, q_norm, head_dim, H3_GPU_BF16, "Q norm") ||
+        !hk_require_active(gpu))
+        return 0;
+    if (head_dim != HK_HD)
+        return hk_fail(gpu, "attention with the Q norm in the kernel supports "
+                            "head_dim 128 (got %u)", head_dim);
+    hk_op_begin(gpu, "attention_cross");
+    if (!hk_attention_bf16(gpu, HK_CBF16(query), HK_CBF16(key),
+                           HK_CBF16(value), HK_BF16(output), q_rows, kv_rows,
+                           heads, head_dim, scale, 0, 0, NULL, NULL, 0,
+                           HK_CBF16(q_norm), NULL, NULL, epsilon))
+        return 0;
+    return hk_op_end(gpu, "attention_cross", HK_KIND_SDPA);
 }
 
 int h3_hip_sdpa_rope_bf16(h3_gpu *gpu, h3_gpu_tensor *output,

@@ -160,7 +160,10 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
                       uint32_t q_rows, uint32_t kv_rows, uint32_t heads,
                       uint32_t head_dim, float scale, int head_major,
                       int sparse, const uint16_t *rope_cos = nullptr,
-                      const uint16_t *rope_sin = nullptr, int fused_qkv = 0);
+                      const uint16_t *rope_sin = nullptr, int fused_qkv = 0,
+                      const uint16_t *q_norm = nullptr,
+                      const uint16_t *q_cos = nullptr,
+                      const uint16_t *q_sin = nullptr, float q_eps = 0.0f);
 /* The two-pass reference attention (any head size up to 16384 keys). */
 int hk_attention_reference(struct h3_gpu *gpu, const uint16_t *q,
                            const uint16_t *k, const uint16_t *v, uint16_t *o,

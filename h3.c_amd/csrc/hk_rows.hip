@@ -575,8 +575,10 @@ __device__ __forceinline__ void hk_pack_store(uint16_t *p, const float v[DPL]) {
  * elements of qkv (query must be qkv itself; key and value are unused), and
  * V stays where it is: attention then reads all three from the fused
  * buffer (h3_hip_sdpa_qkv_bf16).  Each thread reads its elements before any
- * thread of its row group writes. */
-template <int DPL, bool IN_PLACE = false>
+ * thread of its row group writes.  K_ONLY (with IN_PLACE): K alone, for
+ * attention that normalises and rotates Q itself as it loads it
+ * (h3_hip_sdpa_qkv_norm_rope_bf16). */
+template <int DPL, bool IN_PLACE = false, bool K_ONLY = false>
 __global__ void __launch_bounds__(256)
 hk_qk_norm_rope128v(const uint16_t *qkv,
                     const uint16_t *__restrict__ q_weight,
@@ -607,7 +609,12 @@ hk_qk_norm_rope128v(const uint16_t *qkv,
     }
     const uint32_t d0 = part * DPL;
     float q[DPL], k[DPL], qw[DPL], kw[DPL];
-    hk_unpack<DPL>(qkv + q_base + d0, q);
+    if (K_ONLY) {
+#pragma unroll
+        for (int e = 0; e < DPL; e++) q[e] = 0.0f;
+    } else {
+        hk_unpack<DPL>(qkv + q_base + d0, q);
+    }
     hk_unpack<DPL>(qkv + k_base + d0, k);
     vec_t vr;
     if (!IN_PLACE) vr = *(const vec_t *)(qkv + v_base + d0);
@@ -669,7 +676,7 @@ hk_qk_norm_rope128v(const uint16_t *qkv,
     }
     const size_t out = ((size_t)row * heads + head) * HD + d0;
     if (IN_PLACE) {
-        hk_pack_store<DPL>(query + q_base + d0, qo);
+        if (!K_ONLY) hk_pack_store<DPL>(query + q_base + d0, qo);
         hk_pack_store<DPL>(query + k_base + d0, ko);
         return;
     }
@@ -1755,7 +1762,7 @@ int h3_hip_qk_norm_rope_inplace_bf16(h3_gpu *gpu, h3_gpu_tensor *qkv,
                                      const h3_gpu_tensor *rope_sin,
                                      uint32_t sequence, uint32_t heads,
                                      uint32_t head_dim, uint32_t rope_half,
-                                     float epsilon) {
+                                     float epsilon, int keys_only) {
     const size_t count = (size_t)sequence * heads * head_dim;
     if (!HK_REQ_BF16(qkv, count * 3, "QKV") ||
         !HK_REQ_BF16(q_norm, head_dim, "Q norm") ||
@@ -1775,7 +1782,15 @@ int h3_hip_qk_norm_rope_inplace_bf16(h3_gpu *gpu, h3_gpu_tensor *qkv,
                             "tensors (got %u / %u)", head_dim, rope_half);
     hk_op_begin(gpu, "qk_norm_rope_inplace");
     const size_t vectors = (size_t)sequence * heads;
-    if (vectors)
+    if (vectors && keys_only)
+        hipLaunchKernelGGL((hk_qk_norm_rope128v<8, true, true>),
+                           dim3((unsigned)((vectors + 15) / 16)), dim3(256), 0,
+                           gpu->stream, HK_CBF16(qkv), HK_CBF16(q_norm),
+                           HK_CBF16(k_norm), HK_CBF16(rope_cos),
+                           HK_CBF16(rope_sin), HK_BF16(qkv), (uint16_t *)NULL,
+                           (uint16_t *)NULL, sequence, heads, rope_half, 0u,
+                           epsilon);
+    else if (vectors)
         hipLaunchKernelGGL((hk_qk_norm_rope128v<8, true>),
                            dim3((unsigned)((vectors + 15) / 16)), dim3(256), 0,
                            gpu->stream, HK_CBF16(qkv), HK_CBF16(q_norm),

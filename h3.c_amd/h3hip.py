@@ -132,7 +132,11 @@ def lib():
         "h3_hip_sdpa_rope_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _U32, _U32,
                                        _U32, _U32, _F]),
         "h3_hip_qk_norm_rope_inplace_bf16": (_I, [_P, _P, _P, _P, _P, _P, _U32,
-                                                  _U32, _U32, _U32, _F]),
+                                                  _U32, _U32, _U32, _F, _I]),
+        "h3_hip_sdpa_qkv_norm_rope_bf16": (_I, [_P, _P, _P, _P, _P, _P, _U32,
+                                                _U32, _U32, _U32, _F, _F]),
+        "h3_hip_sdpa_cross_norm_bf16": (_I, [_P, _P, _P, _P, _P, _P, _U32,
+                                             _U32, _U32, _U32, _F, _F]),
         "h3_hip_sdpa_qkv_bf16": (_I, [_P, _P, _P, _U32, _U32, _U32, _F]),
         "h3_hip_linear_group_table": (_P, [_P, _P, _P, _P, _U32, _U32, _U32,
                                            _U32]),

@@ -527,11 +527,13 @@ static int run_wan_block(h3hip_dit *dit, uint32_t index, int fuse_next) {
            DIT_OP(K_ROWS, h3_hip_qk_norm_rope_inplace_bf16(
                            gpu, dit->qkv, w->q_norm, w->k_norm, dit->rope_cos,
                            dit->rope_sin, rows, c->heads, c->head_dim,
-                           c->rope_half, eps),
-                  "Q/K norm + RoPE (in place)") &&
-           DIT_OP(K_ATTN, h3_hip_sdpa_qkv_bf16(gpu, dit->attn, dit->qkv, rows,
-                                            c->heads, c->head_dim, scale),
-                  "self-attention") &&
+                           c->rope_half, eps, 1),
+                  "K norm + RoPE (in place)") &&
+           DIT_OP(K_ATTN, h3_hip_sdpa_qkv_norm_rope_bf16(
+                           gpu, dit->attn, dit->qkv, w->q_norm,
+                           dit->rope_cos, dit->rope_sin, rows, c->heads,
+                           c->head_dim, c->rope_half, eps, scale),
+                  "self-attention (Q norm + RoPE in the kernel)") &&
            DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->proj, dit->attn, w->out,
                                           w->out_bias, rows, inner, d),
                   "self-attention output") &&
@@ -543,15 +545,11 @@ static int run_wan_block(h3hip_dit *dit, uint32_t index, int fuse_next) {
            DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->cross_q, dit->mod_b,
                                           w->cq, w->cq_bias, rows, d, inner),
                   "cross Q projection") &&
-           DIT_OP(K_ROWS, h3_gpu_head_rms_norm_bf16(gpu, dit->cross_q,
-                                                 w->cq_norm, rows, c->heads,
-                                                 c->head_dim, eps),
-                  "cross Q norm") &&
-           DIT_OP(K_ATTN, h3_gpu_sdpa_cross_bf16(gpu, dit->cross_out,
-                                              dit->cross_q, w->ctx_k,
-                                              w->ctx_v, rows, t, c->heads,
-                                              c->head_dim, scale),
-                  "cross-attention") &&
+           DIT_OP(K_ATTN, h3_hip_sdpa_cross_norm_bf16(
+                           gpu, dit->cross_out, dit->cross_q, w->ctx_k,
+                           w->ctx_v, w->cq_norm, rows, t, c->heads,
+                           c->head_dim, eps, scale),
+                  "cross-attention (Q norm in the kernel)") &&
            DIT_OP(K_GEMM, h3_gpu_linear_bf16(gpu, dit->proj, dit->cross_out,
                                           w->co, w->co_bias, rows, inner, d),
                   "cross-attention output") &&

@@ -85,7 +85,10 @@ int h3_hip_qk_norm_rope_inplace_bf16(h3_gpu *gpu, h3_gpu_tensor *qkv,
                                      const h3_gpu_tensor *rope_sin,
                                      uint32_t sequence, uint32_t heads,
                                      uint32_t head_dim, uint32_t rope_half,
-                                     float epsilon);
+                                     float epsilon, int keys_only);
+
+/* The same over K alone (keys_only != 0) leaves Q as the projection wrote
+ * it, for h3_hip_sdpa_qkv_norm_rope_bf16. */
 
 /* h3_gpu_sdpa_bf16 with Q, K and V read from the fused rows
  * [sequence][3][heads][head_dim] (as left by
@@ -95,6 +98,39 @@ int h3_hip_qk_norm_rope_inplace_bf16(h3_gpu *gpu, h3_gpu_tensor *qkv,
 int h3_hip_sdpa_qkv_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
                          const h3_gpu_tensor *qkv, uint32_t sequence,
                          uint32_t heads, uint32_t head_dim, float scale);
+
+/* h3_hip_sdpa_qkv_bf16 on fused rows whose Q is still as the projection
+ * wrote it (K normalised and rotated, e.g. by the keys-only in-place
+ * pass): the attention kernel applies Q's per-head RMS norm (weight
+ * q_norm, epsilon) and, with rope_cos / rope_sin ([sequence][48] bf16, or
+ * both NULL), the RoPE pairs (d, d + 48) as it loads Q -- the arithmetic
+ * and rounding of h3_gpu_qkv_rope_bf16 (reference h3_cuda_attention.cu:
+ * 190-245), so the result equals normalising and rotating Q first.  Needs
+ * head_dim 128 and 16-byte aligned tensors.  No reference counterpart;
+ * used by this backend's Wan-shaped block. */
+int h3_hip_sdpa_qkv_norm_rope_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                                   const h3_gpu_tensor *qkv,
+                                   const h3_gpu_tensor *q_norm,
+                                   const h3_gpu_tensor *rope_cos,
+                                   const h3_gpu_tensor *rope_sin,
+                                   uint32_t sequence, uint32_t heads,
+                                   uint32_t head_dim, uint32_t rope_half,
+                                   float epsilon, float scale);
+
+/* h3_gpu_sdpa_cross_bf16 with the per-head RMS norm of Q (weight q_norm,
+ * epsilon) applied by the attention kernel as it loads Q: the arithmetic
+ * and rounding of h3_gpu_head_rms_norm_bf16, so the result equals
+ * normalising Q first.  Needs head_dim 128 and 16-byte aligned tensors.
+ * No reference counterpart (the reference has no cross-attention); used
+ * by this backend's Wan-shaped block. */
+int h3_hip_sdpa_cross_norm_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                                const h3_gpu_tensor *query,
+                                const h3_gpu_tensor *key,
+                                const h3_gpu_tensor *value,
+                                const h3_gpu_tensor *q_norm, uint32_t q_rows,
+                                uint32_t kv_rows, uint32_t heads,
+                                uint32_t head_dim, float epsilon,
+                                float scale);
 
 /* LayerNorm adaLN:
  *   n = (x - mean) * rsqrt(var + eps) [* w + b]      (w, b may be NULL)

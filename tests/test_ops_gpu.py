@@ -458,7 +458,7 @@ def test_qkv_in_place_and_fused_attention(gpu, seq, heads):
             ts, seq, heads, hd, rope_half, C.c_float(1e-5))
     fused = gpu.bf16(qkv)
     gpu.run("h3_hip_qk_norm_rope_inplace_bf16", fused, tqw, tkw, tc, ts, seq,
-            heads, hd, rope_half, C.c_float(1e-5))
+            heads, hd, rope_half, C.c_float(1e-5), 0)
     rows = gpu.read_bf16(fused).view(np.uint16).reshape(seq, 3, heads * hd)
     q = gpu.read_bf16(tq).view(np.uint16).reshape(seq, heads * hd)
     k = gpu.read_bf16(tk).view(np.uint16).reshape(seq, heads * hd)
@@ -474,6 +474,64 @@ def test_qkv_in_place_and_fused_attention(gpu, seq, heads):
                           gpu.read_bf16(joint).view(np.uint16))
 
 
+@pytest.mark.parametrize("seq,heads", [(45, 3), (300, 2), (2378, 4)])
+def test_q_norm_rope_in_attention(gpu, seq, heads):
+    """h3_hip_sdpa_qkv_norm_rope_bf16 on rows whose K alone was normalised
+    and rotated in place equals normalising and rotating Q and K in place
+    first and calling h3_hip_sdpa_qkv_bf16, bit for bit: the attention
+    kernel repeats the row kernel's sums, rounding and RoPE exactly."""
+    hd, rope_half = 128, 48
+    rng = np.random.default_rng(7 * seq + heads)
+    qkv = rand_bf16(rng, seq * 3 * heads * hd, 2.0)
+    qw, kw = rand_bf16(rng, hd, 0.1, 1.0), rand_bf16(rng, hd, 0.1, 1.0)
+    ang = rng.uniform(-30, 30, seq * rope_half).astype(np.float32)
+    cos, sin = oracle.bf16(np.cos(ang)), oracle.bf16(np.sin(ang))
+    tqw, tkw, tc, ts = gpu.bf16(qw), gpu.bf16(kw), gpu.bf16(cos), gpu.bf16(sin)
+    eps, scale = C.c_float(1e-6), C.c_float(1.0 / math.sqrt(hd))
+    both, keys = gpu.bf16(qkv), gpu.bf16(qkv)
+    gpu.run("h3_hip_qk_norm_rope_inplace_bf16", both, tqw, tkw, tc, ts, seq,
+            heads, hd, rope_half, eps, 0)
+    gpu.run("h3_hip_qk_norm_rope_inplace_bf16", keys, tqw, tkw, tc, ts, seq,
+            heads, hd, rope_half, eps, 1)
+    rows_b = gpu.read_bf16(both).view(np.uint16).reshape(seq, 3, -1)
+    rows_k = gpu.read_bf16(keys).view(np.uint16).reshape(seq, 3, -1)
+    assert np.array_equal(rows_b[:, 1:], rows_k[:, 1:])
+    assert np.array_equal(rows_k[:, 0],
+                          qkv.view(np.uint16).reshape(seq, 3, -1)[:, 0])
+    n = seq * heads * hd
+    want, got = gpu.new_bf16(n), gpu.new_bf16(n)
+    gpu.run("h3_hip_sdpa_qkv_bf16", want, both, seq, heads, hd, scale)
+    gpu.run("h3_hip_sdpa_qkv_norm_rope_bf16", got, keys, tqw, tc, ts, seq,
+            heads, hd, rope_half, eps, scale)
+    assert np.array_equal(gpu.read_bf16(want).view(np.uint16),
+                          gpu.read_bf16(got).view(np.uint16))
+
+
+@pytest.mark.parametrize("q_rows,kv_rows,heads", [(300, 77, 2), (1000, 512, 3),
+                                                  (70, 513, 2)])
+def test_cross_q_norm_in_attention(gpu, q_rows, kv_rows, heads):
+    """h3_hip_sdpa_cross_norm_bf16 equals h3_gpu_head_rms_norm_bf16 on Q
+    followed by h3_gpu_sdpa_cross_bf16, bit for bit."""
+    hd = 128
+    rng = np.random.default_rng(q_rows + kv_rows + heads)
+    q = rand_bf16(rng, q_rows * heads * hd, 3.0)
+    k = rand_bf16(rng, kv_rows * heads * hd)
+    v = rand_bf16(rng, kv_rows * heads * hd)
+    w = rand_bf16(rng, hd, 0.1, 1.0)
+    tq, tk, tv, tw = gpu.bf16(q), gpu.bf16(k), gpu.bf16(v), gpu.bf16(w)
+    eps, scale = C.c_float(1e-6), C.c_float(1.0 / math.sqrt(hd))
+    n = q_rows * heads * hd
+    want, got = gpu.new_bf16(n), gpu.new_bf16(n)
+    normed = gpu.bf16(q)
+    gpu.run("h3_gpu_head_rms_norm_bf16", normed, tw, q_rows, heads, hd, eps)
+    gpu.run("h3_gpu_sdpa_cross_bf16", want, normed, tk, tv, q_rows, kv_rows,
+            heads, hd, scale)
+    gpu.run("h3_hip_sdpa_cross_norm_bf16", got, tq, tk, tv, tw, q_rows,
+            kv_rows, heads, hd, eps, scale)
+    assert np.array_equal(gpu.read_bf16(want).view(np.uint16),
+                          gpu.read_bf16(got).view(np.uint16))
+
+
 def test_qkv_in_place_rejects_other_shapes(gpu):
     seq, heads, hd = 8, 2, 64
     buf = gpu.new_bf16(seq * 3 * heads * hd)
@@ -482,7 +540,7 @@ def test_qkv_in_place_rejects_other_shapes(gpu):
     gpu.begin()
     ok = gpu.L.h3_hip_qk_norm_rope_inplace_bf16(gpu.h, buf, w, w, tab, tab,
                                                 seq, heads, hd, 16,
-                                                C.c_float(1e-5))
+                                                C.c_float(1e-5), 0)
     gpu.submit()
     assert not ok and "head_dim 128" in gpu.error()
 
