@@ -247,7 +247,8 @@ def attention_sweep(gpu):
     same attention on pre-rotated Q/K without it
     (h3_gpu_sdpa_bf16, the kernel the blocks use after their Q/K norm +
     RoPE pass); cross-attention of those queries against 512 keys.  HIP
-    events around 10 launches each."""
+    events around 10 launches each, in two alternating passes, the faster
+    kept."""
     import ctypes as C
     L = gpu.L
     out = {}
@@ -274,7 +275,10 @@ def attention_sweep(gpu):
             tc, ts = gpu.bf16(cos), gpu.bf16(sin)
         variants = ((name, "rope"), (name + "_no_rope", "plain")) if grid \
             else ((name, "cross"),)
-        for label, mode in variants:
+        best = {}
+        # two alternating passes, the faster of each kept: the first launches
+        # after the fills run slow whichever variant comes first
+        for label, mode in variants * 2:
             def launch():
                 if mode == "rope":
                     return L.h3_hip_sdpa_rope_bf16(gpu.h, to, tq, tk, tv, tc,
@@ -298,6 +302,9 @@ def attention_sweep(gpu):
             ms = C.c_double()
             L.h3_hip_marker_elapsed(gpu.h, 6, 7, C.byref(ms))
             t = ms.value / reps
+            if label in best and best[label] <= t:
+                continue
+            best[label] = t
             tf = 4.0 * q_rows * kv_rows * heads * 128 / (t / 1e3) / 1e12
             out[label] = {"us": round(t * 1e3, 1), "tflops": round(tf, 1),
                           "frac_of_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
