@@ -63,11 +63,13 @@ OPS_GEMM, OPS_ACT, OPS_ATTN, OPS_ROWS, OPS_CTX = 1, 2, 4, 8, 16
 
 
 KERNEL_NAMES = {
-    "gemm_plain": "hk_gemm_mfma<0> (QKV, out, cross q, cross out, FFN "
+    "gemm_plain": "hk_gemm_mfma<0, false> (QKV, out, cross q, cross out, FFN "
                   "down)",
-    "gemm_gelu": "hk_gemm_mfma<2> + split tail (FFN up + GELU)",
-    "context_kv": "split-K hk_gemm_mfma<3> + reduce (cross K/V of the text)",
-    "attention": "hk_flash_fwd<false, false> (self + cross)",
+    "gemm_gelu": "hk_gemm_mfma<2, false> + split tail (FFN up + GELU)",
+    "context_kv": "grouped hk_gemm_mfma<0, true>: the text's cross K/V of "
+                  "all blocks in one launch",
+    "attention": "hk_flash_fwd<false, false, false> (self + cross, Q norm "
+                 "(+ RoPE) applied as Q is loaded)",
     "row_ops": "adaLN / gates / Q-K norm + RoPE / head norm / residual rows",
 }
 
@@ -598,7 +600,7 @@ def main():
                                           BF16_PEAK_TFLOPS, 4)}
                    if fl else {}))
             for name, (ms, fl) in cls.items()},
-        "roofline": {"kernel": "hk_gemm_mfma<0> (plain-epilogue GEMMs of "
+        "roofline": {"kernel": "hk_gemm_mfma<0, false> (plain-epilogue GEMMs of "
                                "the forward)",
                      "bound": "mfma",
                      "achieved": round(per_launch_flops / (per_launch_ms /
