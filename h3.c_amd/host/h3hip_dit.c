@@ -29,7 +29,7 @@ struct h3hip_dit {
     /* shared state and activations */
     h3_gpu_tensor *hidden, *row_map, *rope_cos, *rope_sin, *context;
     h3_gpu_tensor *mod_a, *mod_b, *qkv, *query, *key, *value, *attn, *proj;
-    h3_gpu_tensor *cross_q, *cross_k, *cross_v, *cross_out, *ffn_act;
+    h3_gpu_tensor *cross_q, *cross_out, *ffn_act;
     /* Wan: the grouped projection's table, problems (block b's K, V) at
      * 2 b and 2 b + 1 */
     h3_gpu_tensor *ctx_table;
@@ -196,16 +196,17 @@ h3hip_dit *h3hip_dit_create(h3_gpu *gpu, const h3hip_dit_config *config,
     dit->mod_a = bf16(dit, n * d, &ok);
     dit->mod_b = bf16(dit, n * d, &ok);
     dit->qkv = bf16(dit, n * 3 * inner, &ok);
-    dit->query = bf16(dit, n * inner, &ok);
-    dit->key = bf16(dit, n * inner, &ok);
-    dit->value = bf16(dit, n * inner, &ok);
+    if (!is_wan(dit)) {
+        /* the Wan block attends straight from the fused QKV rows */
+        dit->query = bf16(dit, n * inner, &ok);
+        dit->key = bf16(dit, n * inner, &ok);
+        dit->value = bf16(dit, n * inner, &ok);
+    }
     dit->attn = bf16(dit, n * inner, &ok);
     dit->proj = bf16(dit, n * d, &ok);
     if (is_wan(dit)) {
         dit->context = bf16(dit, t * d, &ok);
         dit->cross_q = bf16(dit, n * inner, &ok);
-        dit->cross_k = bf16(dit, t * inner, &ok);
-        dit->cross_v = bf16(dit, t * inner, &ok);
         dit->cross_out = bf16(dit, n * inner, &ok);
         dit->ffn_act = bf16(dit, n * f, &ok);
     }
@@ -264,7 +265,7 @@ void h3hip_dit_free(h3hip_dit *dit) {
         dit->hidden, dit->row_map, dit->rope_cos, dit->rope_sin,
         dit->context, dit->mod_a, dit->mod_b, dit->qkv, dit->query,
         dit->key, dit->value, dit->attn, dit->proj, dit->cross_q,
-        dit->cross_k, dit->cross_v, dit->cross_out, dit->ffn_act,
+        dit->cross_out, dit->ffn_act,
         dit->ctx_table};
     for (size_t i = 0; i < sizeof(shared) / sizeof(*shared); i++)
         h3_gpu_tensor_free(shared[i]);
