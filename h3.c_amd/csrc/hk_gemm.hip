@@ -126,31 +126,12 @@ struct hk_gemm_args {
     uint32_t pair_tiles;
     const uint16_t *w1, *bias1;
     uint16_t *c1;
-    /* The GROUP kernel's problems, HK_GROUP_WORDS 64-bit words each: X, W,
-     * bias, C, then m | x_bytes << 32 and first_tile | tiles << 32.
-     *   group_tiles > 0: problems of one shape and one X (g.x, g.m): tile t
-     *     is tile t % group_tiles of problem t / group_tiles;
-     *   group_tiles == 0: group_pieces pieces of problems with one N and K
-     *     but their own X and M, each a run of `tiles` tiles of its problem
-     *     from first_tile, dealt out in order. */
-    uint32_t group_tiles, group_pieces;
+    /* a group of problems of one shape and one X (the GROUP kernel): tile
+     * t is tile t % group_tiles of problem t / group_tiles, whose W, bias
+     * and C are group[3 p], group[3 p + 1], group[3 p + 2] */
+    uint32_t group_tiles;
     const uint64_t *group;
 };
-#define HK_GROUP_WORDS 6
-
-/* A word of the GROUP kernel's problem table, read with a uniform index:
- * marked uniform so that the buffer resources built from it stay in
- * scalar registers (a table load otherwise counts as divergent and every
- * buffer load becomes a loop over lanes). */
-__device__ __forceinline__ uint64_t hk_group_word(const uint64_t *table,
-                                                  uint32_t index) {
-    const uint64_t v = table[index];
-    /* readfirstlane returns int: widen through uint32_t, not sign-extend */
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
-    const uint32_t hi =
-        (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return (uint64_t)lo | ((uint64_t)hi << 32);
-}
 
 /* Tile index -> (tile_m, tile_n): column bands of HK_GROUP_M row tiles, so
  * consecutive tiles share W rows (and, band by band, X rows). */
@@ -202,32 +183,11 @@ hk_gemm_mfma(hk_gemm_args g) {
     /* grouped: the problem's bias and C addresses are read again by the
      * epilogue, so that only the index stays live through the main loop */
     uint32_t prob = 0;
-    const uint16_t *x_p = g.x;
-    uint32_t m_p = g.m, x_bytes_p = g.x_bytes;
     if (GROUP) {
-        if (g.group_tiles) {
-            prob = pid / g.group_tiles;
-            pid -= prob * g.group_tiles;
-        } else {
-            uint32_t base = 0;
-            for (;;) {
-                const uint32_t run = (uint32_t)(
-                    hk_group_word(g.group, HK_GROUP_WORDS * prob + 5) >> 32);
-                if (pid < base + run || prob + 1 >= g.group_pieces) break;
-                base += run;
-                prob++;
-            }
-            const uint32_t at = HK_GROUP_WORDS * prob;
-            pid = pid - base + (uint32_t)hk_group_word(g.group, at + 5);
-            x_p = (const uint16_t *)hk_group_word(g.group, at);
-            const uint64_t mx = hk_group_word(g.group, at + 4);
-            m_p = (uint32_t)mx;
-            x_bytes_p = (uint32_t)(mx >> 32);
-        }
-        wsrc = (const uint16_t *)hk_group_word(g.group,
-                                               HK_GROUP_WORDS * prob + 1);
+        prob = pid / g.group_tiles;
+        pid -= prob * g.group_tiles;
+        wsrc = (const uint16_t *)g.group[3 * prob];
     }
-    const uint32_t tiles_m_p = GROUP ? (m_p + HK_BM - 1) / HK_BM : g.tiles_m;
     if (partial) {
         split = pid / g.part_tiles;
         part = pid - split * g.part_tiles;
@@ -237,7 +197,7 @@ hk_gemm_mfma(hk_gemm_args g) {
         k_first = split * g.split_steps;
     }
     uint32_t tile_m, tile_n;
-    hk_tile_coords(pid, tiles_m_p, g.tiles_n, tile_m, tile_n);
+    hk_tile_coords(pid, g.tiles_m, g.tiles_n, tile_m, tile_n);
     const uint32_t m0 = tile_m * HK_BM;
 
     /* ---- staging plan ----
@@ -248,7 +208,7 @@ hk_gemm_mfma(hk_gemm_args g) {
      * p / 8, physical chunk p % 8, holding logical chunk (p % 8) ^ key(row).
      * Rows past M (and W rows past the end) get an offset beyond the
      * buffer, which the hardware returns as zeros. */
-    const __amdgpu_buffer_rsrc_t xr = hk_rsrc(x_p, x_bytes_p);
+    const __amdgpu_buffer_rsrc_t xr = hk_rsrc(g.x, g.x_bytes);
     const __amdgpu_buffer_rsrc_t wr = hk_rsrc(wsrc, g.w_bytes);
     uint32_t x_off[8], w_off[8];
 #pragma unroll
@@ -256,7 +216,7 @@ hk_gemm_mfma(hk_gemm_args g) {
         const uint32_t slot = (wave * 8u + j) * 64u + lane;
         const uint32_t row = slot >> 3;
         const uint32_t chunk = (slot & 7u) ^ hk_swz_key(row);
-        const uint32_t xm = min(m0 + row, m_p);
+        const uint32_t xm = min(m0 + row, g.m);
         x_off[j] = xm * g.k * 2u + chunk * 16u + k_first * (HK_BK * 2u);
         uint32_t wrow;
         if (swiglu_rows) {
@@ -451,16 +411,8 @@ hk_gemm_mfma(hk_gemm_args g) {
         return;
     }
     const uint16_t *bias_p =
-        GROUP ? (const uint16_t *)hk_group_word(g.group,
-                                                HK_GROUP_WORDS * prob + 2)
-              : g.bias;
-    uint16_t *c_p =
-        GROUP ? (uint16_t *)hk_group_word(g.group, HK_GROUP_WORDS * prob + 3)
-              : g.c;
-    const uint32_t m_e =
-        GROUP && !g.group_tiles
-            ? (uint32_t)hk_group_word(g.group, HK_GROUP_WORDS * prob + 4)
-            : g.m;
+        GROUP ? (const uint16_t *)g.group[3 * prob + 1] : g.bias;
+    uint16_t *c_p = GROUP ? (uint16_t *)g.group[3 * prob + 2] : g.c;
     constexpr uint32_t tile_cols = EPI == HK_EPI_SWIGLU ? 128u : HK_BN;
     constexpr uint32_t pitch = tile_cols * 2u;     /* bytes per LDS row */
     constexpr uint32_t chunks = pitch / 16u;
@@ -561,7 +513,7 @@ hk_gemm_mfma(hk_gemm_args g) {
 #pragma unroll
         for (int u = 0; u < 8; u++) {
             const uint32_t m = m0 + row0 + u * rows_per_pass;
-            if (m >= m_e || col >= g.n) continue;
+            if (m >= g.m || col >= g.n) continue;
             uint16_t *dst = c_p + (size_t)m * g.n + col;
             if (col + 8u <= g.n)
                 __builtin_nontemporal_store(
@@ -908,7 +860,7 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
         g.part_tiles = 0;
         g.tile_count = g.tiles_m * g.tiles_n;
         g.pair_tiles = 0;
-        g.group_tiles = g.group_pieces = 0;
+        g.group_tiles = 0;
         g.group = NULL;
         g.w1 = g.bias1 = NULL;
         g.c1 = NULL;
@@ -1056,7 +1008,7 @@ int hk_gemm_bf16_pair(struct h3_gpu *gpu, const uint16_t *x,
     g.tile_count = parts * splits;
     g.pair_tiles = tiles;
     g.w1 = w1; g.bias1 = b1; g.c1 = c1;
-    g.group_tiles = g.group_pieces = 0;
+    g.group_tiles = 0;
     g.group = NULL;
     hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_PARTIAL>, dim3(parts * splits),
                        dim3(HK_GEMM_THREADS), HK_GEMM_LDS, gpu->stream, g);
@@ -1089,29 +1041,6 @@ static int hk_gemm_bf16_group(struct h3_gpu *gpu, const uint16_t *x,
     hipLaunchKernelGGL((hk_gemm_mfma<HK_EPI_STORE, true>),
                        dim3(hk_gemm_grid(g.tile_count, cus)),
                        dim3(HK_GEMM_THREADS), HK_GEMM_LDS, gpu->stream, g);
-    return 1;
-}
-
-/* Pieces of problems of one N and K with their own X and M (device table
- * of HK_GROUP_WORDS words per piece), `tiles` tiles in all, in one
- * data-parallel launch. */
-static int hk_gemm_bf16_mix(struct h3_gpu *gpu, const uint64_t *table,
-                            uint32_t count, uint32_t tiles, uint32_t n,
-                            uint32_t k) {
-    if (!count || !tiles) return 1;
-    hk_gemm_lds_setup(gpu);
-    hk_gemm_args g;
-    memset(&g, 0, sizeof(g));
-    g.n = n; g.k = k;
-    g.tiles_n = (n + HK_BN - 1) / HK_BN;
-    g.w_bytes = (uint32_t)((uint64_t)n * k * 2);
-    g.group_pieces = count;
-    g.group = table;
-    g.tile_count = tiles;
-    const uint32_t cus = gpu->num_cus > 0 ? (uint32_t)gpu->num_cus : 256u;
-    hipLaunchKernelGGL((hk_gemm_mfma<HK_EPI_STORE, true>),
-                       dim3(hk_gemm_grid(tiles, cus)), dim3(HK_GEMM_THREADS),
-                       HK_GEMM_LDS, gpu->stream, g);
     return 1;
 }
 
@@ -1230,7 +1159,7 @@ h3_gpu_tensor *h3_hip_linear_group_table(h3_gpu *gpu,
         hk_fail(gpu, "grouped linear table needs at least one problem");
         return NULL;
     }
-    uint64_t *entries = (uint64_t *)calloc((size_t)count * HK_GROUP_WORDS, sizeof(uint64_t));
+    uint64_t *entries = (uint64_t *)calloc((size_t)count * 3, sizeof(uint64_t));
     if (!entries) {
         hk_fail(gpu, "out of host memory");
         return NULL;
@@ -1257,15 +1186,12 @@ h3_gpu_tensor *h3_hip_linear_group_table(h3_gpu *gpu,
                          "the MFMA kernel, or sizes out of its range", p);
             return NULL;
         }
-        entries[HK_GROUP_WORDS * p + 1] =
-            (uint64_t)(uintptr_t)weights[p]->data;
-        entries[HK_GROUP_WORDS * p + 2] =
-            bias ? (uint64_t)(uintptr_t)bias->data : 0;
-        entries[HK_GROUP_WORDS * p + 3] =
-            (uint64_t)(uintptr_t)outputs[p]->data;
+        entries[3 * p] = (uint64_t)(uintptr_t)weights[p]->data;
+        entries[3 * p + 1] = bias ? (uint64_t)(uintptr_t)bias->data : 0;
+        entries[3 * p + 2] = (uint64_t)(uintptr_t)outputs[p]->data;
     }
     h3_gpu_tensor *table = h3_gpu_tensor_from_u32(
-        gpu, (const uint32_t *)entries, (size_t)count * HK_GROUP_WORDS * 2);
+        gpu, (const uint32_t *)entries, (size_t)count * 6);
     free(entries);
     return table;
 }
@@ -1274,15 +1200,14 @@ int h3_hip_linear_group_bf16(h3_gpu *gpu, const h3_gpu_tensor *table,
                              uint32_t first, uint32_t count,
                              const h3_gpu_tensor *input, uint32_t rows,
                              uint32_t input_dim, uint32_t output_dim) {
-    if (!hk_require(gpu, table,
-                    ((size_t)first + count) * HK_GROUP_WORDS * 2, H3_GPU_U32,
+    if (!hk_require(gpu, table, ((size_t)first + count) * 6, H3_GPU_U32,
                     "grouped linear table") ||
         !hk_require(gpu, input, (size_t)rows * input_dim, H3_GPU_BF16,
                     "grouped linear input") ||
         !hk_require_active(gpu))
         return 0;
     if (!count) return 1;
-    const uint64_t *dev = (const uint64_t *)table->data + (size_t)first * HK_GROUP_WORDS;
+    const uint64_t *dev = (const uint64_t *)table->data + (size_t)first * 3;
     const bool mfma = rows > 64 &&
                       hk_gemm_mfma_ok(gpu, input->data, input->data, NULL,
                                       input->data, rows, output_dim,
@@ -1296,10 +1221,10 @@ int h3_hip_linear_group_bf16(h3_gpu *gpu, const h3_gpu_tensor *table,
         /* reference kernels (or a shape the MFMA kernel does not take):
          * the problems one by one, from a host copy of the table */
         uint64_t *entries =
-            (uint64_t *)calloc((size_t)count * HK_GROUP_WORDS, sizeof(uint64_t));
+            (uint64_t *)calloc((size_t)count * 3, sizeof(uint64_t));
         if (!entries) return hk_fail(gpu, "out of host memory");
         hipError_t status = hipMemcpyAsync(
-            entries, dev, (size_t)count * HK_GROUP_WORDS * sizeof(uint64_t),
+            entries, dev, (size_t)count * 3 * sizeof(uint64_t),
             hipMemcpyDeviceToHost, gpu->stream);
         if (status == hipSuccess) status = hipStreamSynchronize(gpu->stream);
         if (status != hipSuccess) {
@@ -1309,103 +1234,15 @@ int h3_hip_linear_group_bf16(h3_gpu *gpu, const h3_gpu_tensor *table,
         }
         for (uint32_t p = 0; p < count && ok; p++)
             ok = hk_gemm_bf16(gpu, HK_CBF16(input),
-                              (const uint16_t *)(uintptr_t)
-                                  entries[HK_GROUP_WORDS * p + 1],
-                              (const uint16_t *)(uintptr_t)
-                                  entries[HK_GROUP_WORDS * p + 2],
-                              (uint16_t *)(uintptr_t)
-                                  entries[HK_GROUP_WORDS * p + 3], rows,
+                              (const uint16_t *)(uintptr_t)entries[3 * p],
+                              (const uint16_t *)(uintptr_t)entries[3 * p + 1],
+                              (uint16_t *)(uintptr_t)entries[3 * p + 2], rows,
                               output_dim, input_dim, HK_EPI_STORE);
         free(entries);
     }
     if (!ok) return 0;
     return hk_op_end(gpu, "gemm_group",
                      hk_linear_kind(rows, input_dim, output_dim));
-}
-
-uint32_t h3_hip_linear_idle_tiles(h3_gpu *gpu, uint32_t rows,
-                                  uint32_t output_dim) {
-    if (!gpu || !rows || !output_dim) return 0;
-    const uint32_t cus = gpu->num_cus > 0 ? (uint32_t)gpu->num_cus : 256u;
-    const uint32_t tiles =
-        ((rows + HK_BM - 1) / HK_BM) * ((output_dim + HK_BN - 1) / HK_BN);
-    const uint32_t rounds = (tiles + cus - 1) / cus;
-    return rounds * cus - tiles;
-}
-
-h3_gpu_tensor *h3_hip_linear_mix_table(h3_gpu *gpu,
-                                       const h3_hip_linear_piece *pieces,
-                                       uint32_t count, uint32_t input_dim,
-                                       uint32_t output_dim) {
-    if (!gpu) return NULL;
-    if (!count || !pieces) {
-        hk_fail(gpu, "mixed linear table needs at least one piece");
-        return NULL;
-    }
-    const uint32_t tiles_n = (output_dim + HK_BN - 1) / HK_BN;
-    uint64_t *entries =
-        (uint64_t *)calloc((size_t)count * HK_GROUP_WORDS, sizeof(uint64_t));
-    if (!entries) {
-        hk_fail(gpu, "out of host memory");
-        return NULL;
-    }
-    for (uint32_t p = 0; p < count; p++) {
-        const h3_hip_linear_piece *c = &pieces[p];
-        const uint64_t problem_tiles =
-            (uint64_t)((c->rows + HK_BM - 1) / HK_BM) * tiles_n;
-        const char *why = NULL;
-        if (!hk_require(gpu, c->input, (size_t)c->rows * input_dim,
-                        H3_GPU_BF16, "mixed linear input") ||
-            !hk_require(gpu, c->weight, (size_t)output_dim * input_dim,
-                        H3_GPU_BF16, "mixed linear weight") ||
-            !hk_require(gpu, c->output, (size_t)c->rows * output_dim,
-                        H3_GPU_BF16, "mixed linear output") ||
-            (c->bias && !hk_require(gpu, c->bias, output_dim, H3_GPU_BF16,
-                                    "mixed linear bias"))) {
-            free(entries);
-            return NULL;
-        }
-        if (c->rows <= 64 || gpu->reference_kernels ||
-            !hk_gemm_mfma_ok(gpu, c->input->data, c->weight->data,
-                             c->bias ? c->bias->data : NULL, c->output->data,
-                             c->rows, output_dim, input_dim, HK_EPI_STORE))
-            why = "needs over 64 rows, the MFMA kernel and its alignment";
-        else if (!c->tiles || (uint64_t)c->first_tile + c->tiles > problem_tiles)
-            why = "tile range outside its problem";
-        if (why) {
-            free(entries);
-            hk_fail(gpu, "mixed linear piece %u %s", p, why);
-            return NULL;
-        }
-        const uint64_t x_bytes = (uint64_t)c->rows * input_dim * 2;
-        uint64_t *e = entries + (size_t)HK_GROUP_WORDS * p;
-        e[0] = (uint64_t)(uintptr_t)c->input->data;
-        e[1] = (uint64_t)(uintptr_t)c->weight->data;
-        e[2] = c->bias ? (uint64_t)(uintptr_t)c->bias->data : 0;
-        e[3] = (uint64_t)(uintptr_t)c->output->data;
-        e[4] = (uint64_t)c->rows | (x_bytes << 32);
-        e[5] = (uint64_t)c->first_tile | ((uint64_t)c->tiles << 32);
-    }
-    h3_gpu_tensor *table = h3_gpu_tensor_from_u32(
-        gpu, (const uint32_t *)entries, (size_t)count * HK_GROUP_WORDS * 2);
-    free(entries);
-    return table;
-}
-
-int h3_hip_linear_mix_bf16(h3_gpu *gpu, const h3_gpu_tensor *table,
-                           uint32_t count, uint32_t tiles, uint32_t input_dim,
-                           uint32_t output_dim) {
-    if (!hk_require(gpu, table, (size_t)count * HK_GROUP_WORDS * 2,
-                    H3_GPU_U32, "mixed linear table") ||
-        !hk_require_active(gpu))
-        return 0;
-    if (input_dim % HK_BK || output_dim % 4)
-        return hk_fail(gpu, "mixed linear needs K %% 64 == 0 and N %% 4 == 0");
-    hk_op_begin(gpu, "gemm_mix");
-    if (!hk_gemm_bf16_mix(gpu, (const uint64_t *)table->data, count, tiles,
-                          output_dim, input_dim))
-        return 0;
-    return hk_op_end(gpu, "gemm_mix", HK_KIND_LINEAR);
 }
 
 int h3_hip_linear_pair_bf16(h3_gpu *gpu, h3_gpu_tensor *output0,

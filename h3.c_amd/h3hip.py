@@ -142,9 +142,6 @@ def lib():
                                            _U32]),
         "h3_hip_linear_group_bf16": (_I, [_P, _P, _U32, _U32, _P, _U32, _U32,
                                           _U32]),
-        "h3_hip_linear_idle_tiles": (_U32, [_P, _U32, _U32]),
-        "h3_hip_linear_mix_table": (_P, [_P, _P, _U32, _U32, _U32]),
-        "h3_hip_linear_mix_bf16": (_I, [_P, _P, _U32, _U32, _U32, _U32]),
         "h3_gpu_layer_adaln_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _U32,
                                          _U32, _U32, _U32, _U32, _F]),
         "h3_gpu_gate_layer_adaln_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P,

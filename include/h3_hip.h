@@ -189,36 +189,6 @@ int h3_hip_linear_group_bf16(h3_gpu *gpu, const h3_gpu_tensor *table,
                              const h3_gpu_tensor *input, uint32_t rows,
                              uint32_t input_dim, uint32_t output_dim);
 
-/* Pieces of projections that share N (output_dim) and K (input_dim) but
- * not their input or row count, as one data-parallel launch: piece p
- * computes tiles [first_tile, first_tile + tiles) of its output = input .
- * weight^T + bias, counting the output's 256 x 256 tiles row band by row
- * band of 8 tile rows, column by column within a band (the order the GEMM
- * deals them in).  Each tile is exactly what h3_gpu_linear_bf16's
- * data-parallel kernel computes for it.  h3_hip_linear_mix_table checks
- * the pieces (over 64 rows each, the MFMA kernel's alignment) and returns
- * the device table (free it with h3_gpu_tensor_free; it stays valid while
- * the tensors live); h3_hip_linear_mix_bf16 launches it, `tiles` being the
- * pieces' total.  h3_hip_linear_idle_tiles gives the tile slots a linear
- * of that output shape leaves idle in its last round (one 256 x 256 tile
- * per CU at a time), which such pieces can fill for free.  No reference
- * counterpart: the Wan-shaped driver computes the next block's text K/V
- * in the idle slots of its 6144 x 5120 x 5120 projections. */
-typedef struct {
-    h3_gpu_tensor *output;
-    const h3_gpu_tensor *input, *weight, *bias; /* bias may be NULL */
-    uint32_t rows, first_tile, tiles;
-} h3_hip_linear_piece;
-uint32_t h3_hip_linear_idle_tiles(h3_gpu *gpu, uint32_t rows,
-                                  uint32_t output_dim);
-h3_gpu_tensor *h3_hip_linear_mix_table(h3_gpu *gpu,
-                                       const h3_hip_linear_piece *pieces,
-                                       uint32_t count, uint32_t input_dim,
-                                       uint32_t output_dim);
-int h3_hip_linear_mix_bf16(h3_gpu *gpu, const h3_gpu_tensor *table,
-                           uint32_t count, uint32_t tiles, uint32_t input_dim,
-                           uint32_t output_dim);
-
 /* Two projections of one input, output0 = X . weight0^T + bias0 and
  * output1 = X . weight1^T + bias1, each exactly as h3_gpu_linear_bf16
  * computes it (f32 accumulation, one bf16 rounding).  Small launches

@@ -140,64 +140,6 @@ def test_linear_group(gpu, m, k, n, count, first, exact):
         gpu.L.h3_gpu_tensor_free(table)
 
 
-def _tile_region(t, rows, n, group_m=8):
-    """Rows and columns of tile t of a rows x n output in the GEMM's tile
-    order: bands of group_m tile rows, column by column within a band."""
-    tiles_m, tiles_n = -(-rows // 256), -(-n // 256)
-    band = group_m * tiles_n
-    first_m = (t // band) * group_m
-    band_rows = min(tiles_m - first_m, group_m)
-    tm = first_m + (t % band) % band_rows
-    tn = (t % band) // band_rows
-    return (slice(tm * 256, min(rows, tm * 256 + 256)),
-            slice(tn * 256, min(n, tn * 256 + 256)))
-
-
-def test_linear_mix(gpu):
-    """h3_hip_linear_mix_bf16: pieces of three projections with their own
-    inputs and row counts in one launch; every tile a piece covers equals
-    h3_gpu_linear_bf16's (data-parallel at K = 448, so bit for bit), every
-    other tile is left alone."""
-    k, n = 448, 768
-    rng = np.random.default_rng(5)
-    specs = [(600, 0, 9), (300, 2, 3), (2100, 5, 20)]   # rows, first, tiles
-    P = C.c_void_p
-    pieces, outs, refs, before = [], [], [], []
-    for rows, first, tiles in specs:
-        x, w, b = (rand_bf16(rng, rows * k), rand_bf16(rng, n * k, 0.05),
-                   rand_bf16(rng, n, 0.1))
-        tx, tw, tb = gpu.bf16(x), gpu.bf16(w), gpu.bf16(b)
-        to, ref = gpu.new_bf16(rows * n), gpu.new_bf16(rows * n)
-        gpu.run("h3_gpu_fill_normal_bf16", to, 0, rows * n, 9, 0.0, 1.0)
-        gpu.run("h3_gpu_linear_bf16", ref, tx, tw, tb, rows, k, n)
-        before.append(gpu.read_bf16(to).view(np.uint16).reshape(rows, n).copy())
-        refs.append(gpu.read_bf16(ref).view(np.uint16).reshape(rows, n))
-        outs.append(to)
-        pieces.append((to, tx, tw, tb, rows, first, tiles))
-
-    class Piece(C.Structure):
-        _fields_ = [("output", P), ("input", P), ("weight", P), ("bias", P),
-                    ("rows", C.c_uint32), ("first_tile", C.c_uint32),
-                    ("tiles", C.c_uint32)]
-    arr = (Piece * len(pieces))(*[Piece(*p) for p in pieces])
-    table = gpu.L.h3_hip_linear_mix_table(gpu.h, C.cast(arr, P), len(pieces),
-                                          k, n)
-    assert table, gpu.error()
-    try:
-        total = sum(t for _, _, t in specs)
-        gpu.run("h3_hip_linear_mix_bf16", table, len(pieces), total, k, n)
-        for (rows, first, tiles), to, ref, old in zip(specs, outs, refs,
-                                                       before):
-            got = gpu.read_bf16(to).view(np.uint16).reshape(rows, n)
-            want = old.copy()
-            for t in range(first, first + tiles):
-                r, c = _tile_region(t, rows, n)
-                want[r, c] = ref[r, c]
-            assert np.array_equal(got, want), (rows, first, tiles)
-    finally:
-        gpu.L.h3_gpu_tensor_free(table)
-
-
 def test_linear_stats_kind(gpu):
     """Routing-shape rule of the stats counters (reference
     h3_cuda_core.cu:838-841): rows >= 32, in >= 256, out >= 256 -> kind 1."""
