@@ -133,6 +133,20 @@ struct hk_gemm_args {
     const uint64_t *group;
 };
 
+/* A word of the GROUP kernel's problem table, read with a uniform index:
+ * marked uniform so that the buffer resources built from it stay in
+ * scalar registers (a table load otherwise counts as divergent, and every
+ * buffer load would become a loop over the lanes' descriptors). */
+__device__ __forceinline__ uint64_t hk_group_word(const uint64_t *table,
+                                                  uint32_t index) {
+    const uint64_t v = table[index];
+    /* readfirstlane returns int: widen through uint32_t, not sign-extend */
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi =
+        (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (uint64_t)lo | ((uint64_t)hi << 32);
+}
+
 /* Tile index -> (tile_m, tile_n): column bands of HK_GROUP_M row tiles, so
  * consecutive tiles share W rows (and, band by band, X rows). */
 __device__ __forceinline__ void hk_tile_coords(uint32_t tile, uint32_t tiles_m,
@@ -186,7 +200,7 @@ hk_gemm_mfma(hk_gemm_args g) {
     if (GROUP) {
         prob = pid / g.group_tiles;
         pid -= prob * g.group_tiles;
-        wsrc = (const uint16_t *)g.group[3 * prob];
+        wsrc = (const uint16_t *)hk_group_word(g.group, 3 * prob);
     }
     if (partial) {
         split = pid / g.part_tiles;
@@ -411,8 +425,10 @@ hk_gemm_mfma(hk_gemm_args g) {
         return;
     }
     const uint16_t *bias_p =
-        GROUP ? (const uint16_t *)g.group[3 * prob + 1] : g.bias;
-    uint16_t *c_p = GROUP ? (uint16_t *)g.group[3 * prob + 2] : g.c;
+        GROUP ? (const uint16_t *)hk_group_word(g.group, 3 * prob + 1)
+              : g.bias;
+    uint16_t *c_p =
+        GROUP ? (uint16_t *)hk_group_word(g.group, 3 * prob + 2) : g.c;
     constexpr uint32_t tile_cols = EPI == HK_EPI_SWIGLU ? 128u : HK_BN;
     constexpr uint32_t pitch = tile_cols * 2u;     /* bytes per LDS row */
     constexpr uint32_t chunks = pitch / 16u;
