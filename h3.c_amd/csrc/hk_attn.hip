@@ -108,7 +108,7 @@ struct hk_attn_args {
      * (running max in the exp2 domain, sum) into part_ml[pid][256] */
     uint32_t full_units, pieces;
     float *part_o, *part_ml;
-    /* ROPE: the joint sequence's cos / sin tables packed per (row, dim) as
+    /* RoPE: the joint sequence's cos / sin tables packed per (row, dim) as
      * the two bf16 pairs (c, -s), (s, c) of the rotation ([rows][48]
      * uint64, hk_rope_pack); Q arrives unrotated and is rotated as the
      * kernel loads its fragments, K was rotated by hk_rope_keys */
@@ -213,7 +213,7 @@ hk_rope_keys(const uint16_t *k, const uint64_t *table, uint16_t *out,
     dst[c1] = y;
 }
 
-template <bool SPARSE, bool SPLIT, bool ROPE>
+template <bool SPARSE, bool SPLIT>
 __global__ void __launch_bounds__(HK_THREADS, HK_WG_PER_CU)
 hk_flash_fwd(hk_attn_args a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t hk_lds[];
@@ -230,10 +230,12 @@ hk_flash_fwd(hk_attn_args a) {
 
     const __amdgpu_buffer_rsrc_t qr = hk_attn_rsrc(a.q, a.q_bytes);
     __amdgpu_buffer_rsrc_t tr;
-    if (ROPE) tr = hk_attn_rsrc(a.rope_pk, a.rope_bytes);
+    /* a runtime branch (once per workgroup) rather than a template
+     * argument: a separate instance came out 3-5% slower in its main loop */
+    if (a.rope_pk) tr = hk_attn_rsrc(a.rope_pk, a.rope_bytes);
 
     /* ---- Q fragments: B operand of S^T = K . Q^T ----
-     * k-step ks: Q[q][16 ks + 8 half .. +8]; with ROPE, dims d < 48 pair
+     * k-step ks: Q[q][16 ks + 8 half .. +8]; with the RoPE table, dims d < 48 pair
      * with d + 48, i.e. k-step ks < 3 with ks + 3 in the same lane */
     const uint32_t qbase = qblock * HK_QB + wave * 32u;
     hk_bf16x8 qf[8];
@@ -247,7 +249,7 @@ hk_flash_fwd(hk_attn_args a) {
         for (int ks = 0; ks < 8; ks++)
             raw[ks] = __builtin_amdgcn_raw_buffer_load_b128(
                 qr, off == 0xfffffff0u ? off : off + ks * 32u, 0, 0);
-        if (ROPE) {
+        if (a.rope_pk) {
             /* dims 16 ks + 8 half + e, e < 8: 64 bytes of the table */
             const uint32_t roff = q < a.q_rows
                 ? (q * HK_ROPE_HALF + half * 8u) * 8u : 0xfffffff0u;
@@ -360,7 +362,7 @@ hk_flash_fwd(hk_attn_args a) {
      * K and V go from global memory straight into LDS with direct-to-LDS
      * buffer loads: wave w fills rows 8 w .. 8 w + 7 of a tile in two
      * 1-KiB loads, lane l writing physical chunk l & 15 of row 4 i + l / 16;
-     * the swizzles are applied on the global side.  (With ROPE, K arrives
+     * the swizzles are applied on the global side.  (With the RoPE table, K arrives
      * already rotated by hk_rope_keys.) */
     uint32_t k_dma_off[HK_DMA], v_dma_off[HK_DMA];
 #pragma unroll
@@ -739,29 +741,23 @@ __global__ void __launch_bounds__(256) hk_flash_combine(hk_attn_args a) {
  * raised */
 static uint64_t hk_attn_lds_ready = 0;
 
-template <bool SPARSE, bool SPLIT, bool ROPE>
+template <bool SPARSE, bool SPLIT>
 static void hk_flash_set_lds() {
     (void)hipFuncSetAttribute(
-        (const void *)hk_flash_fwd<SPARSE, SPLIT, ROPE>,
+        (const void *)hk_flash_fwd<SPARSE, SPLIT>,
         hipFuncAttributeMaxDynamicSharedMemorySize, HK_ATTN_LDS);
 }
 
 template <bool SPLIT>
 static void hk_flash_launch(struct h3_gpu *gpu, const hk_attn_args &a,
-                            bool masked, bool rope, uint32_t grid) {
+                            bool masked, uint32_t grid) {
     const dim3 g(grid), b(HK_THREADS);
-    if (masked && rope)
-        hipLaunchKernelGGL((hk_flash_fwd<true, SPLIT, true>), g, b,
-                           HK_ATTN_LDS, gpu->stream, a);
-    else if (masked)
-        hipLaunchKernelGGL((hk_flash_fwd<true, SPLIT, false>), g, b,
-                           HK_ATTN_LDS, gpu->stream, a);
-    else if (rope)
-        hipLaunchKernelGGL((hk_flash_fwd<false, SPLIT, true>), g, b,
-                           HK_ATTN_LDS, gpu->stream, a);
+    if (masked)
+        hipLaunchKernelGGL((hk_flash_fwd<true, SPLIT>), g, b, HK_ATTN_LDS,
+                           gpu->stream, a);
     else
-        hipLaunchKernelGGL((hk_flash_fwd<false, SPLIT, false>), g, b,
-                           HK_ATTN_LDS, gpu->stream, a);
+        hipLaunchKernelGGL((hk_flash_fwd<false, SPLIT>), g, b, HK_ATTN_LDS,
+                           gpu->stream, a);
 }
 
 int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
@@ -815,14 +811,10 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
     if (flash) {
         const uint64_t lds_bit = 1ull << (gpu->device & 63);
         if (!(hk_attn_lds_ready & lds_bit)) {
-            hk_flash_set_lds<false, false, false>();
-            hk_flash_set_lds<true, false, false>();
-            hk_flash_set_lds<false, true, false>();
-            hk_flash_set_lds<true, true, false>();
-            hk_flash_set_lds<false, false, true>();
-            hk_flash_set_lds<true, false, true>();
-            hk_flash_set_lds<false, true, true>();
-            hk_flash_set_lds<true, true, true>();
+            hk_flash_set_lds<false, false>();
+            hk_flash_set_lds<true, false>();
+            hk_flash_set_lds<false, true>();
+            hk_flash_set_lds<true, true>();
             hk_attn_lds_ready |= lds_bit;
         }
         hk_attn_args a;
@@ -908,9 +900,9 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
             }
         }
         if (a.full_units)
-            hk_flash_launch<false>(gpu, a, masked, rope, a.full_units);
+            hk_flash_launch<false>(gpu, a, masked, a.full_units);
         if (pieces > 1) {
-            hk_flash_launch<true>(gpu, a, masked, rope, tail * pieces);
+            hk_flash_launch<true>(gpu, a, masked, tail * pieces);
             hipLaunchKernelGGL(hk_flash_combine, dim3(tail * (HK_QB / 8)),
                                dim3(256),
                                0, gpu->stream, a);
