@@ -27,12 +27,13 @@
  *     hardware overlaps one wave's softmax (VALU) with the other's MFMAs;
  *   - the grid is 1-D and regrouped per XCD so the query blocks of one head
  *     run on one XCD and share its L2 copy of that head's K and V;
- *   - the softmax is VALU-bound, so its instruction count is kept low: the
- *     running max only moves (rescaling O and l) when a tile's max exceeds
- *     it by more than 2^8, the scale is folded into one FMA per score, row
- *     maxima take two scores per med3 (compiler-visible, so the MFMA ->
- *     VALU result hazards get their wait states), and the key-range mask
- *     is compiled only into the last tile's step.
+ *   - the softmax is VALU-bound, so its instruction count is kept low:
+ *     P is taken against the running max as it stands and the tile's own
+ *     max is only computed (O and l rescaled) when a P sum passes 2^32,
+ *     the scale is folded into one FMA per score, and the key-range mask
+ *     is compiled only into the last tile's step;
+ *   - the V^T reads are inline assembly (hk_vt_read), so the compiler does
+ *     not wait for the next tile's direct-to-LDS loads before them.
  *
  * A two-pass reference kernel (hk_attn_ref.hip, built with the default
  * floating-point semantics) serves other head sizes, H3_HIP_REFERENCE=1 and
@@ -40,13 +41,13 @@
  */
 #include "hk_common.h"
 #include "hk_internal.h"
+#include "hk_attn.h"
 
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
 #include <type_traits>
 
-#define HK_HD 128
 /* HK_WAVES 4 (two 128-query workgroups per CU, each with its own barrier)
  * also builds and passes the tests; measured against 8 it was 3% slower on
  * self-attention and 9% faster on 512-key cross-attention, so 8 stays */
@@ -57,71 +58,11 @@
 #define HK_QB (HK_WAVES * 32) /* queries per workgroup */
 #define HK_WG_PER_CU (8 / HK_WAVES) /* workgroups per CU: two waves per SIMD */
 #define HK_DMA (16 / HK_WAVES) /* 1-KiB loads per wave per tile and operand */
-#define HK_KT 64              /* keys per tile */
-#define HK_TILE_BYTES (HK_KT * HK_HD * 2)      /* 16 KiB, 256-B rows */
 #define HK_STAGE_BYTES (2 * HK_TILE_BYTES)     /* K tile, then V tile */
 #define HK_ATTN_LDS (2 * HK_STAGE_BYTES)       /* 64 KiB */
-#define HK_ROPE_HALF 48       /* RoPE pairs (d, d + 48), d < 48 */
 
-typedef int hk_v4i __attribute__((ext_vector_type(4)));
-typedef int hk_v2i __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) void hk_lds_void;
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t hk_attn_rsrc(
-    const void *base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base),
-                                             (short)0, (int)bytes,
-                                             0x00020000);
-}
 
-/* K tile: row = key (256 B = 16 chunks of 16 B); logical chunk c of row r
- * sits at physical chunk c ^ (r & 15), so the 32-key fragment reads (one
- * chunk of 16 consecutive rows per 16 lanes) hit 16 distinct chunks. */
-__device__ __forceinline__ uint32_t hk_k_swz(uint32_t row, uint32_t chunk) {
-    return row * 256u + ((chunk ^ (row & 15u)) << 4);
-}
-
-/* V tile: row-major like K, chunk c of row r at c ^ 4 (r & 3).  The
- * transposing reads take 4 consecutive rows x 32 B per 16 lanes; the XOR
- * puts the four rows' 32-byte pieces in four different 64-byte bank
- * groups. */
-__device__ __forceinline__ uint32_t hk_v_swz(uint32_t row, uint32_t chunk) {
-    return row * 256u + ((chunk ^ ((row & 3u) << 2)) << 4);
-}
-
-struct hk_attn_args {
-    const uint16_t *q, *k, *v;
-    uint16_t *o;
-    uint32_t q_rows, kv_rows, heads, q_blocks;
-    /* bytes readable from q, k and v; elements from one Q / K / V row to
-     * the next (heads * 128, or 3 heads * 128 when the three are read from
-     * the fused QKV projection output) */
-    uint32_t q_bytes, kv_bytes, v_bytes, in_stride;
-    float scale_log2;
-    int head_major;
-    /* block-sparse mask: CSR over 128-row query blocks of 64-row key tiles
-     * (lists sorted), or null for dense */
-    const uint32_t *sparse_ptr, *sparse_idx;
-    uint32_t sparse_blocks; /* query blocks in the CSR */
-    /* split launch (SPLIT): work item full_units + pid / pieces, key tiles
-     * of piece pid % pieces; unnormalised f32 O into part_o[pid][256][128],
-     * (running max in the exp2 domain, sum) into part_ml[pid][256] */
-    uint32_t full_units, pieces;
-    float *part_o, *part_ml;
-    /* RoPE: the joint sequence's cos / sin tables packed per (row, dim) as
-     * the two bf16 pairs (c, -s), (s, c) of the rotation ([rows][48]
-     * uint64, hk_rope_pack); Q arrives unrotated and is rotated as the
-     * kernel loads its fragments, K was rotated by hk_rope_keys */
-    const uint64_t *rope_pk;
-    uint32_t rope_bytes;
-    /* Q_NORM: the per-head RMS norm of Q (weight q_norm[128], epsilon
-     * q_eps) applied as the Q fragments are loaded, then, with q_cos /
-     * q_sin ([rows][48] bf16), the RoPE pairs (d, d + 48) -- the arithmetic
-     * and rounding of hk_head_rms128 / hk_qk_norm_rope128v, so the result
-     * equals normalising (and rotating) Q first */
-    const uint16_t *q_norm, *q_cos, *q_sin;
-    float q_eps;
-};
 
 /* The reference's RoPE pair rotation (h3_cuda_attention.cu:218-233) on 8
  * pairs, x' = x c - y s and y' = y c + x s, rounded to bf16.  With bf16
@@ -511,18 +452,21 @@ hk_flash_fwd(hk_attn_args a) {
             }
         }
 
-        /* online softmax per query column.  The running maximum is only
-         * moved (and O, l rescaled) when a score exceeds it by more than
-         * 2^8 in the exp2 domain; otherwise P = exp2(s - m_stale) <= 256.
-         * The stale maximum is not the row's true maximum and the gap
-         * between them is not a power of two, so bf16(P) can round
-         * differently from the reference's P (relative to the row maximum)
-         * by up to half a bf16 ulp per element: O matches to the bf16
-         * rounding of P (the bound the tests apply), while l, summed over
-         * the unrounded P, is exact up to f32 rounding. */
+        /* online softmax per query column.  P = exp2(s - m_run) is taken
+         * against the running maximum m_run as it stands; the tile's own
+         * maximum is only computed, and m_run moved (O and l rescaled),
+         * when that leaves a lane's P sum above 2^32 (some score above
+         * m_run + 32 in the exp2 domain) or m_run is still unset.  So P <=
+         * 2^32 always, which keeps O and l far from f32 overflow, and the
+         * common tile runs its exponentials straight off the scores.  The
+         * stale maximum is not the row's true maximum and the gap between
+         * them is not a power of two, so bf16(P) can round differently
+         * from the reference's P (relative to the row maximum) by up to
+         * half a bf16 ulp per element: O matches to the bf16 rounding of P
+         * (the bound the tests apply), while l, summed over the unrounded
+         * P, is exact up to f32 rounding. */
         const uint32_t kv0 = tile * HK_KT;
         hk_bf16x8 pf[2][2]; /* [kt][step] */
-        float mx = -INFINITY;
         if constexpr (tail) {
 #pragma unroll
             for (int kt = 0; kt < 2; kt++)
@@ -533,23 +477,47 @@ hk_flash_fwd(hk_attn_args a) {
                     if (key >= a.kv_rows) s[kt][r] = -INFINITY;
                 }
         }
+        auto exps = [&]() -> float {
+            const float neg = -m_run;
+            float sum = 0.0f;
 #pragma unroll
-        for (int kt = 0; kt < 2; kt++)
+            for (int kt = 0; kt < 2; kt++) {
+                float p[16];
 #pragma unroll
-            for (int r = 0; r < 16; r += 2)
-                mx = __builtin_fmaxf(
-                    mx, __builtin_fmaxf(s[kt][r], s[kt][r + 1]));
-        /* the column's other 16 keys sit in the lane 32 away: one
-         * v_permlane32_swap (no LDS round trip) hands each half the other's
-         * value */
-        {
+                for (int r = 0; r < 16; r++) {
+                    p[r] = __builtin_amdgcn_exp2f(
+                        __builtin_fmaf(s[kt][r], a.scale_log2, neg));
+                    sum += p[r];
+                }
+#pragma unroll
+                for (int st = 0; st < 2; st++) {
+                    hk_bf16x8 v;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[e] = (__bf16)p[st * 8 + e];
+                    pf[kt][st] = v;
+                }
+            }
+            return sum;
+        };
+        /* (with m_run unset the sum is not looked at: it may hold
+         * inf - inf) */
+        const bool unset = m_run == -INFINITY;
+        float sum = unset ? 0.0f : exps();
+        if (__builtin_amdgcn_ballot_w64(unset || sum > 0x1p32f)) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+                for (int r = 0; r < 16; r += 2)
+                    mx = __builtin_fmaxf(
+                        mx, __builtin_fmaxf(s[kt][r], s[kt][r + 1]));
+            /* the column's other 16 keys sit in the lane 32 away: one
+             * v_permlane32_swap (no LDS round trip) hands each half the
+             * other's value */
             const auto sw = __builtin_amdgcn_permlane32_swap(
                 __float_as_uint(mx), __float_as_uint(mx), false, false);
             mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) *
                  a.scale_log2;
-        }
-        const bool grow = mx > m_run + 8.0f;
-        if (__builtin_amdgcn_ballot_w64(grow)) {
             const float m_new = fmaxf(m_run, mx);
             const float ref = m_new == -INFINITY ? 0.0f : m_new;
             const float c = __builtin_amdgcn_exp2f(m_run - ref);
@@ -559,50 +527,37 @@ hk_flash_fwd(hk_attn_args a) {
             for (int d = 0; d < 4; d++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) o[d][r] *= c;
-        }
-        const float neg = -m_run;
-        float sum = 0.0f;
-#pragma unroll
-        for (int kt = 0; kt < 2; kt++) {
-            float p[16];
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                p[r] = __builtin_amdgcn_exp2f(
-                    __builtin_fmaf(s[kt][r], a.scale_log2, neg));
-                sum += p[r];
-            }
-#pragma unroll
-            for (int st = 0; st < 2; st++) {
-                hk_bf16x8 v;
-#pragma unroll
-                for (int e = 0; e < 8; e++) v[e] = (__bf16)p[st * 8 + e];
-                pf[kt][st] = v;
-            }
+            sum = exps();
         }
         l_part += sum;
 
         /* O^T[d] += V^T[d, keys] . P^T[keys]: the V^T operand comes from
-         * the row-major V tile through two transposing 8-byte reads */
+         * the row-major V tile through two transposing 8-byte reads per
+         * fragment, a 16-key step's four fragments read while the MFMAs
+         * of the step before run (hk_vt_read) */
+        hk_v2i vt[2][4][2];
+        hk_vt_read(vt[0], v_frag, stage * HK_STAGE_BYTES);
 #pragma unroll
-        for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-            for (int st = 0; st < 2; st++) {
-#pragma unroll
-                for (int d = 0; d < 4; d++) {
-                    const uint32_t at = v_frag[d] + stage * HK_STAGE_BYTES +
-                                        (kt * 32u + st * 16u) * 256u;
-                    const hk_bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-                        (__attribute__((address_space(3))) hk_bf16x4 *)(
-                            uintptr_t)at);
-                    const hk_bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-                        (__attribute__((address_space(3))) hk_bf16x4 *)(
-                            uintptr_t)(at + 8u * 256u));
-                    const hk_bf16x8 vf = {lo[0], lo[1], lo[2], lo[3],
-                                          hi[0], hi[1], hi[2], hi[3]};
-                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                        vf, pf[kt][st], o[d], 0, 0, 0);
-                }
+        for (int i = 0; i < 4; i++) {
+            const int kt = i >> 1, st = i & 1;
+            if (i < 3) {
+                hk_vt_read(vt[(i + 1) & 1], v_frag,
+                           stage * HK_STAGE_BYTES +
+                               (((i + 1) >> 1) * 32u + ((i + 1) & 1) * 16u) *
+                                   256u);
+                hk_vt_wait<8>(vt[i & 1]);
+            } else {
+                hk_vt_wait<0>(vt[i & 1]);
             }
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                const hk_v4i both = {vt[i & 1][d][0][0], vt[i & 1][d][0][1],
+                                     vt[i & 1][d][1][0], vt[i & 1][d][1][1]};
+                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    __builtin_bit_cast(hk_bf16x8, both), pf[kt][st], o[d], 0,
+                    0, 0);
+            }
+        }
         } /* mine */
 
         /* the next stage's direct-to-LDS loads (issued by every wave) have
