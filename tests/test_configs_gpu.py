@@ -276,6 +276,40 @@ def test_h3_50_block_drift_against_oracle(gpu):
         dit.close()
 
 
+def test_wan_50_block_drift_against_oracle(gpu):
+    """The Wan stack's drift through 50 blocks (hidden 512, 4 heads, 300
+    video + 77 text rows): the hidden state after blocks 9, 19, 29, 39 and
+    49 against the oracle over the same blocks (the reference's full-step
+    checkpoints, tests/test_real_dit_block.c:539-552, 653-662).  The device
+    runs the stack in five calls of ten blocks, each fusing the FFN gate
+    with the next block's adaLN across its blocks and starting with the
+    grouped launch of its blocks' text K/V; each oracle segment starts from
+    the oracle's own previous output."""
+    rows, text, hidden, heads, ffn, blocks = 300, 77, 512, 4, 1024, 50
+    cfg = h3hip.dit_config(h3hip.FAMILY_WAN, hidden, heads, ffn, rows,
+                           blocks=blocks, text_rows=text)
+    dit = h3hip.Dit(gpu, cfg)
+    try:
+        dit.init_random(seed=51, weight_std=0.02, mod_std=0.1)
+        rng = np.random.default_rng(51)
+        ang = rng.uniform(-40, 40, rows * 48).astype(np.float32)
+        cos, sin = np.cos(ang), np.sin(ang)
+        dit.set_rope(cos, sin)
+        wts = [{n: dit.read(n, b) for n in WAN_NAMES} for b in range(blocks)]
+        want, ctx = dit.read("hidden"), dit.read("context")
+        zero_map = np.zeros(rows, np.uint32)
+        for first in range(0, blocks, 10):
+            dit.run_blocks(first, 10)
+            got = dit.read("hidden")
+            for w in wts[first:first + 10]:
+                want = oracle.wan_block(want, ctx, w, zero_map,
+                                        oracle.bf16(cos), oracle.bf16(sin),
+                                        rows, text, hidden, heads, ffn)
+            _bar(got, want, f"Wan after block {first + 9}")
+    finally:
+        dit.close()
+
+
 # -------------------------------------------------------------- config 5
 
 def test_config5_denoise_20_steps_reuse_2_matches_oracle(gpu):
