@@ -175,6 +175,52 @@ hk_flash_fwd(hk_attn_args a) {
      * argument: a separate instance came out 3-5% slower in its main loop */
     if (a.rope_pk) tr = hk_attn_rsrc(a.rope_pk, a.rope_bytes);
 
+    /* ---- staging plan ----
+     * K and V go from global memory straight into LDS with direct-to-LDS
+     * buffer loads: wave w fills rows 8 w .. 8 w + 7 of a tile in two
+     * 1-KiB loads, lane l writing physical chunk l & 15 of row 4 i + l / 16;
+     * the swizzles are applied on the global side.  (With the RoPE table, K arrives
+     * already rotated by hk_rope_keys.) */
+    uint32_t k_dma_off[HK_DMA], v_dma_off[HK_DMA];
+#pragma unroll
+    for (int i = 0; i < HK_DMA; i++) {
+        const uint32_t row = (wave * HK_DMA + i) * 4u + (lane >> 4);
+        const uint32_t kc = (lane & 15u) ^ (row & 15u);
+        const uint32_t vc = (lane & 15u) ^ ((row & 3u) << 2);
+        k_dma_off[i] = (row * row_stride + head * HK_HD) * 2u + kc * 16u;
+        v_dma_off[i] = (row * row_stride + head * HK_HD) * 2u + vc * 16u;
+    }
+    auto issue_tile = [&](uint32_t kv0, uint32_t stage) {
+        const size_t base = (size_t)kv0 * row_stride;
+        const uint32_t left = a.kv_bytes - kv0 * row_stride * 2u;
+        const __amdgpu_buffer_rsrc_t vr =
+            hk_attn_rsrc(a.v + base, a.v_bytes - kv0 * row_stride * 2u);
+        uint8_t *st = hk_lds + stage * HK_STAGE_BYTES;
+#pragma unroll
+        for (int i = 0; i < HK_DMA; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                vr, (hk_lds_void *)(st + HK_TILE_BYTES +
+                                    (wave * HK_DMA + i) * 1024u),
+                16, v_dma_off[i], 0, 0, 0);
+        const __amdgpu_buffer_rsrc_t kr = hk_attn_rsrc(a.k + base, left);
+#pragma unroll
+        for (int i = 0; i < HK_DMA; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                kr, (hk_lds_void *)(st + (wave * HK_DMA + i) * 1024u), 16,
+                k_dma_off[i], 0, 0, 0);
+    };
+
+    const uint32_t all_tiles = (a.kv_rows + HK_KT - 1) / HK_KT;
+    /* a split piece covers key tiles [first_tile, dense) */
+    const uint32_t piece_tiles =
+        SPLIT ? (all_tiles + a.pieces - 1) / a.pieces : all_tiles;
+    const uint32_t first_tile = SPLIT ? (pid % a.pieces) * piece_tiles : 0;
+    const uint32_t dense =
+        SPLIT ? min(all_tiles, first_tile + piece_tiles) : all_tiles;
+    /* dense: the first key tile's loads go out before the Q fragments'
+     * (its latency then overlaps theirs) */
+    if constexpr (!SPARSE) issue_tile(first_tile * HK_KT, 0);
+
     /* ---- Q fragments: B operand of S^T = K . Q^T ----
      * k-step ks: Q[q][16 ks + 8 half .. +8]; with the RoPE table, dims d < 48 pair
      * with d + 48, i.e. k-step ks < 3 with ks + 3 in the same lane */
@@ -299,41 +345,6 @@ hk_flash_fwd(hk_attn_args a) {
             qf[ks] = __builtin_bit_cast(hk_bf16x8, raw[ks]);
     }
 
-    /* ---- staging plan ----
-     * K and V go from global memory straight into LDS with direct-to-LDS
-     * buffer loads: wave w fills rows 8 w .. 8 w + 7 of a tile in two
-     * 1-KiB loads, lane l writing physical chunk l & 15 of row 4 i + l / 16;
-     * the swizzles are applied on the global side.  (With the RoPE table, K arrives
-     * already rotated by hk_rope_keys.) */
-    uint32_t k_dma_off[HK_DMA], v_dma_off[HK_DMA];
-#pragma unroll
-    for (int i = 0; i < HK_DMA; i++) {
-        const uint32_t row = (wave * HK_DMA + i) * 4u + (lane >> 4);
-        const uint32_t kc = (lane & 15u) ^ (row & 15u);
-        const uint32_t vc = (lane & 15u) ^ ((row & 3u) << 2);
-        k_dma_off[i] = (row * row_stride + head * HK_HD) * 2u + kc * 16u;
-        v_dma_off[i] = (row * row_stride + head * HK_HD) * 2u + vc * 16u;
-    }
-    auto issue_tile = [&](uint32_t kv0, uint32_t stage) {
-        const size_t base = (size_t)kv0 * row_stride;
-        const uint32_t left = a.kv_bytes - kv0 * row_stride * 2u;
-        const __amdgpu_buffer_rsrc_t vr =
-            hk_attn_rsrc(a.v + base, a.v_bytes - kv0 * row_stride * 2u);
-        uint8_t *st = hk_lds + stage * HK_STAGE_BYTES;
-#pragma unroll
-        for (int i = 0; i < HK_DMA; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                vr, (hk_lds_void *)(st + HK_TILE_BYTES +
-                                    (wave * HK_DMA + i) * 1024u),
-                16, v_dma_off[i], 0, 0, 0);
-        const __amdgpu_buffer_rsrc_t kr = hk_attn_rsrc(a.k + base, left);
-#pragma unroll
-        for (int i = 0; i < HK_DMA; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                kr, (hk_lds_void *)(st + (wave * HK_DMA + i) * 1024u), 16,
-                k_dma_off[i], 0, 0, 0);
-    };
-
     /* fragment addresses (lane parts; the stage and tile sub-block go in
      * the instructions' offset fields) */
     const uint32_t lds_base =
@@ -377,13 +388,6 @@ hk_flash_fwd(hk_attn_args a) {
      * and waves 0-3 (first block) / 4-7 (second block) run the MFMAs and
      * softmax only on tiles of their own block's list.  A list's length is
      * clamped to the dense tile count, as in the reference kernel. */
-    const uint32_t all_tiles = (a.kv_rows + HK_KT - 1) / HK_KT;
-    /* a split piece covers key tiles [first_tile, dense) */
-    const uint32_t piece_tiles =
-        SPLIT ? (all_tiles + a.pieces - 1) / a.pieces : all_tiles;
-    const uint32_t first_tile = SPLIT ? (pid % a.pieces) * piece_tiles : 0;
-    const uint32_t dense =
-        SPLIT ? min(all_tiles, first_tile + piece_tiles) : all_tiles;
     uint32_t ia = 0, ea = 0, ib = 0, eb = 0;
     if (SPARSE) {
         /* 128-row CSR blocks: one per workgroup of 128 queries, two for
@@ -574,7 +578,6 @@ hk_flash_fwd(hk_attn_args a) {
         /* the key-range mask is compiled only into the step of the last
          * tile, the only one with keys past kv_rows */
         const uint32_t n = dense - first_tile;
-        issue_tile(first_tile * HK_KT, 0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         uint32_t i = 0;
