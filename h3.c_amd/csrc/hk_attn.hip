@@ -16,12 +16,12 @@
  *   - O^T = V^T . P^T: the P^T operand is the S^T accumulator itself, packed
  *     to bf16 in place.  The accumulator's key order inside a lane is
  *     {4h..4h+3, 8+4h..8+4h+3, ...}; the V^T operand is read in exactly that
- *     key order (two 8-byte LDS reads), so P never goes through LDS;
- *   - V is transposed once per tile while being staged into LDS
- *     (V^T rows of 64 keys, 136-byte pitch), K is staged row-major with an
- *     XOR swizzle on 16-byte chunks;
+ *     key order from the row-major V tile by gfx950's transposing LDS read
+ *     (two ds_read_b64_tr_b16 per fragment), so P never goes through LDS;
+ *   - K and V are staged row-major by direct-to-LDS loads, with XOR
+ *     swizzles on 16-byte chunks (hk_k_swz, hk_v_swz);
  *   - 8 wave64s x 32 queries = 256 queries per workgroup, 64-key tiles,
- *     double-buffered LDS (2 x 33 KiB) with the next tile's global loads in
+ *     double-buffered LDS (2 x 32 KiB) with the next tile's global loads in
  *     flight during the current tile's 32 MFMAs per wave.  At 32 queries a
  *     wave needs under 256 registers, so two waves share each SIMD and the
  *     hardware overlaps one wave's softmax (VALU) with the other's MFMAs;
