@@ -548,10 +548,15 @@ hk_gemm_mfma(hk_gemm_args g) {
 
 /* Skinny GEMM for M <= 64 rows (the per-block modulation projections:
  * time rows x 2688 against 96768 x 2688 weights).  Bound by streaming W
- * from HBM once, so W never touches LDS and is never re-read: each wave
- * owns 32 W rows (output columns) and reads their MFMA fragments straight
- * from global memory (16 bytes per lane), D - 1 64-wide k steps ahead of
- * the MFMAs.  X (MB x 32 rows) is shared by the workgroup's four waves:
+ * from HBM once, and W is never re-read: each wave owns 32 W rows (output
+ * columns) and loads them into registers D - 1 64-wide k steps ahead of
+ * the MFMAs, as whole 128-byte lines (a load gives lane l chunk l % 8 of
+ * row 8 q + l / 8: eight rows per load, where loading the MFMA fragments
+ * directly touches 32 partial rows per load and runs into the cache-line
+ * request rate, 27% slower).  The lines go through the wave's own 4-KiB
+ * LDS buffer (row-major, the big GEMM's chunk swizzle) and come back out
+ * as MFMA fragments.  X (MB x 32 rows) is shared by the workgroup's four
+ * waves:
  * one DMA load per thread and step stages it into LDS (double-buffered,
  * 128-byte rows with the 16-byte-chunk swizzle of the big GEMM), so L2
  * serves it once per workgroup instead of once per wave.  The step's k
@@ -584,7 +589,8 @@ hk_gemm_skinny(const uint16_t *x, const uint16_t *w, const uint16_t *bias,
                uint32_t x_bytes, uint32_t w_bytes) {
     constexpr int D = 4;
     constexpr uint32_t XSTAGE = MB * 32u * 128u; /* bytes of X per k step */
-    /* two X stages, 2 XSTAGE bytes of dynamic LDS */
+    /* two X stages (2 XSTAGE bytes), then the four waves' 4-KiB W buffers:
+     * 2 XSTAGE + 16 KiB of dynamic LDS */
     extern __shared__ __attribute__((aligned(16))) uint8_t hk_xs[];
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -592,7 +598,13 @@ hk_gemm_skinny(const uint16_t *x, const uint16_t *w, const uint16_t *bias,
     const uint32_t n0 = (blockIdx.x * 4u + wave) * 32u;
     const __amdgpu_buffer_rsrc_t xr = hk_rsrc(x, x_bytes);
     const __amdgpu_buffer_rsrc_t wr = hk_rsrc(w, w_bytes);
-    const uint32_t wo = (min(n0 + row, n) * k + half * 8u) * 2u;
+    uint32_t wo[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        wo[q] = (min(n0 + 8u * q + (lane >> 3), n) * k + (lane & 7u) * 8u) *
+                2u;
+    /* the wave's W buffer, after the two X stages */
+    uint8_t *wbuf = hk_xs + 2u * XSTAGE + wave * 4096u;
     /* X staging: slot p = 256 i + tid holds row p / 8, physical chunk p % 8
      * = logical chunk (p % 8) ^ key(row) */
     uint32_t xo[MB];
@@ -610,7 +622,7 @@ hk_gemm_skinny(const uint16_t *x, const uint16_t *w, const uint16_t *bias,
 #pragma unroll
         for (int q = 0; q < 4; q++)
             wf[slot][q] = __builtin_amdgcn_raw_buffer_load_b128(
-                wr, wo, step * 128u + q * 32u, 0);
+                wr, wo[q], step * 128u, 0);
     };
     /* fragment of X rows mb*32 + row, logical chunk 2q + half */
     auto read_x = [&](int buf, int mb, int q) {
@@ -638,15 +650,33 @@ hk_gemm_skinny(const uint16_t *x, const uint16_t *w, const uint16_t *bias,
                 asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
             else
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();
+            /* the barrier as inline assembly: __syncthreads() would also
+             * wait for every load in flight (vmcnt(0)), the W loads of the
+             * steps ahead included */
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
             if (s + 1 < steps) stage_x((d + 1) & 1, s + 1);
             if (s + 3 < steps) load_w((d + 3) % D, s + 3);
+            /* W(s)'s lines into the wave's buffer and back out as
+             * fragments (a wave's LDS operations run in order: no
+             * barrier) */
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint32_t r = 8u * q + (lane >> 3);
+                *(hk_v4i *)(wbuf + r * 128u +
+                            (((lane & 7u) ^ hk_swz_key(r)) << 4)) = wf[d][q];
+            }
+            hk_v4i wfrag[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                wfrag[q] = *(const hk_v4i *)(
+                    wbuf + row * 128u +
+                    (((2u * q + half) ^ hk_swz_key(row)) << 4));
 #pragma unroll
             for (int q = 0; q < 4; q++)
 #pragma unroll
                 for (int mb = 0; mb < MB; mb++)
                     acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                        __builtin_bit_cast(hk_bf16x8, wf[d][q]),
+                        __builtin_bit_cast(hk_bf16x8, wfrag[q]),
                         read_x(d & 1, mb, q), acc[mb], 0, 0, 0);
         }
     }
@@ -850,12 +880,12 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
     if (mfma && m <= 64 && epilogue == HK_EPI_STORE) {
         if (m <= 32)
             hipLaunchKernelGGL(hk_gemm_skinny<1>, dim3((n + 127) / 128),
-                               dim3(256), 2 * 32 * 128, gpu->stream, x, w,
+                               dim3(256), 2 * 32 * 128 + 16384, gpu->stream, x, w,
                                bias, c, m, n, k, (uint32_t)x_bytes,
                                (uint32_t)w_bytes);
         else
             hipLaunchKernelGGL(hk_gemm_skinny<2>, dim3((n + 127) / 128),
-                               dim3(256), 2 * 64 * 128, gpu->stream, x, w,
+                               dim3(256), 2 * 64 * 128 + 16384, gpu->stream, x, w,
                                bias, c, m, n, k, (uint32_t)x_bytes,
                                (uint32_t)w_bytes);
         return 1;
