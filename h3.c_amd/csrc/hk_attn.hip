@@ -618,16 +618,33 @@ hk_flash_fwd(hk_attn_args a) {
     }
 
     if constexpr (SPLIT) {
-        /* unnormalised partials for the combine kernel */
+        /* unnormalised partials for the combine kernel, through the
+         * wave's 8 KiB of LDS in two halves of 64 dims (16-byte chunk c of
+         * row r at c ^ (r % 16)), leaving as whole 256-byte row halves */
         const uint32_t ql = wave * 32u + col;
-        float *po = a.part_o + ((size_t)pid * HK_QB + ql) * HK_HD;
+        float *pw = (float *)(hk_lds + wave * (32u * 64u * 4u));
 #pragma unroll
-        for (int d = 0; d < 4; d++)
+        for (int hd = 0; hd < 2; hd++) {
 #pragma unroll
-            for (int blk = 0; blk < 4; blk++)
-                *(float4 *)(po + d * 32u + blk * 8u + half * 4u) =
-                    make_float4(o[d][blk * 4 + 0], o[d][blk * 4 + 1],
-                                o[d][blk * 4 + 2], o[d][blk * 4 + 3]);
+            for (int dd = 0; dd < 2; dd++)
+#pragma unroll
+                for (int blk = 0; blk < 4; blk++) {
+                    const int d = 2 * hd + dd;
+                    const uint32_t c = dd * 8u + blk * 2u + half;
+                    *(float4 *)(pw + col * 64u + ((c ^ (col & 15u)) << 2)) =
+                        make_float4(o[d][blk * 4 + 0], o[d][blk * 4 + 1],
+                                    o[d][blk * 4 + 2], o[d][blk * 4 + 3]);
+                }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint32_t r = i * 4u + (lane >> 4), c = lane & 15u;
+                const float4 v =
+                    *(const float4 *)(pw + r * 64u + ((c ^ (r & 15u)) << 2));
+                *(float4 *)(a.part_o +
+                            ((size_t)pid * HK_QB + wave * 32u + r) * HK_HD +
+                            hd * 64u + c * 4u) = v;
+            }
+        }
         const float l = l_part + __shfl_xor(l_part, 32, 64);
         if (half == 0)
             *(float2 *)(a.part_ml + ((size_t)pid * HK_QB + ql) * 2u) =
