@@ -23,6 +23,9 @@
 
 #define HK_ROW_THREADS 256
 #define HK_ROW_CHUNKS 4 /* register-resident rows up to 256*4*8 = 8192 */
+#ifndef HK_K_ITEMS
+#define HK_K_ITEMS 2 /* (row, head) vectors per lane group, in-place K: 2 beat 1, 4 and 8 */
+#endif
 
 /* ------------------------------------------------------------ row kernel */
 
@@ -683,6 +686,82 @@ hk_qk_norm_rope128v(const uint16_t *qkv,
     hk_pack_store<DPL>(query + out, qo);
     hk_pack_store<DPL>(key + out, ko);
     *(vec_t *)(value + out) = vr;
+}
+
+/* K alone, in place over the fused QKV rows (the K_ONLY case of
+ * hk_qk_norm_rope128v<8, true, true>, with the same arithmetic in the same
+ * order): each 16-lane group handles ITEMS consecutive (row, head) vectors
+ * and issues all of their loads before any arithmetic.  With one vector
+ * per group a wave has 1 KiB of K in flight, too little to stream HBM at
+ * full rate. */
+template <int ITEMS>
+__global__ void __launch_bounds__(256)
+hk_k_norm_rope128_inplace(uint16_t *qkv, const uint16_t *__restrict__ k_weight,
+                          const uint16_t *__restrict__ rope_cos,
+                          const uint16_t *__restrict__ rope_sin,
+                          uint32_t sequence, uint32_t heads,
+                          uint32_t rope_half, float epsilon) {
+    constexpr uint32_t HD = 128, DPL = 8, LANES = HD / DPL;
+    const uint32_t group = (blockIdx.x * blockDim.x + threadIdx.x) / LANES;
+    const uint32_t part = threadIdx.x % LANES;
+    const uint32_t d0 = part * DPL;
+    const uint32_t vectors = sequence * heads;
+    const size_t inner = (size_t)heads * HD;
+    uint4 kr[ITEMS], cr[ITEMS], sr[ITEMS];
+    size_t k_base[ITEMS];
+    uint32_t row[ITEMS];
+    const bool roped = d0 < rope_half * 2;
+    const bool first = d0 < rope_half;
+    const uint32_t pair = first ? d0 : d0 - rope_half;
+#pragma unroll
+    for (int it = 0; it < ITEMS; it++) {
+        const uint32_t vec = min(group * ITEMS + it, vectors - 1);
+        row[it] = vec / heads;
+        const uint32_t head = vec % heads;
+        k_base[it] = (size_t)row[it] * inner * 3 + inner + (size_t)head * HD;
+        kr[it] = *(const uint4 *)(qkv + k_base[it] + d0);
+        if (roped) {
+            const size_t table = (size_t)row[it] * rope_half + pair;
+            cr[it] = *(const uint4 *)(rope_cos + table);
+            sr[it] = *(const uint4 *)(rope_sin + table);
+        }
+    }
+    float kw[DPL];
+    hk_unpack8(*(const uint4 *)(k_weight + d0), kw);
+    const uint32_t shift = rope_half / DPL;
+    int src = (int)part;
+    if (d0 < rope_half) src = (int)(part + shift);
+    else if (d0 < rope_half * 2) src = (int)(part - shift);
+#pragma unroll
+    for (int it = 0; it < ITEMS; it++) {
+        float k[DPL];
+        hk_unpack8(kr[it], k);
+        float k_sum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < DPL; e++) k_sum = fmaf(k[e], k[e], k_sum);
+#pragma unroll
+        for (int offset = LANES / 2; offset; offset >>= 1)
+            k_sum += __shfl_xor(k_sum, offset, LANES);
+        const float k_inv = 1.0f / sqrtf(k_sum / (float)HD + epsilon);
+        float kn[DPL], kp[DPL], ko[DPL];
+#pragma unroll
+        for (int e = 0; e < DPL; e++) kn[e] = k[e] * k_inv * kw[e];
+#pragma unroll
+        for (int e = 0; e < DPL; e++) kp[e] = __shfl(kn[e], src, LANES);
+#pragma unroll
+        for (int e = 0; e < DPL; e++) ko[e] = kn[e];
+        if (roped) {
+            float c[DPL], sn[DPL];
+            hk_unpack8(cr[it], c);
+            hk_unpack8(sr[it], sn);
+#pragma unroll
+            for (int e = 0; e < DPL; e++)
+                ko[e] = first ? kn[e] * c[e] - kp[e] * sn[e]
+                              : kn[e] * c[e] + kp[e] * sn[e];
+        }
+        if (group * ITEMS + it < vectors)
+            *(uint4 *)(qkv + k_base[it] + d0) = hk_pack8(ko);
+    }
 }
 
 /* Generic per-element variant for other head sizes (any rope_half with
@@ -1783,12 +1862,12 @@ int h3_hip_qk_norm_rope_inplace_bf16(h3_gpu *gpu, h3_gpu_tensor *qkv,
     hk_op_begin(gpu, "qk_norm_rope_inplace");
     const size_t vectors = (size_t)sequence * heads;
     if (vectors && keys_only)
-        hipLaunchKernelGGL((hk_qk_norm_rope128v<8, true, true>),
-                           dim3((unsigned)((vectors + 15) / 16)), dim3(256), 0,
-                           gpu->stream, HK_CBF16(qkv), HK_CBF16(q_norm),
+        hipLaunchKernelGGL(hk_k_norm_rope128_inplace<HK_K_ITEMS>,
+                           dim3((unsigned)((vectors + 16 * HK_K_ITEMS - 1) /
+                                           (16 * HK_K_ITEMS))),
+                           dim3(256), 0, gpu->stream, HK_BF16(qkv),
                            HK_CBF16(k_norm), HK_CBF16(rope_cos),
-                           HK_CBF16(rope_sin), HK_BF16(qkv), (uint16_t *)NULL,
-                           (uint16_t *)NULL, sequence, heads, rope_half, 0u,
+                           HK_CBF16(rope_sin), sequence, heads, rope_half,
                            epsilon);
     else if (vectors)
         hipLaunchKernelGGL((hk_qk_norm_rope128v<8, true>),
