@@ -20,7 +20,9 @@
  *     (two ds_read_b64_tr_b16 per fragment), so P never goes through LDS;
  *   - K and V are staged row-major by direct-to-LDS loads, with XOR
  *     swizzles on 16-byte chunks (hk_k_swz, hk_v_swz);
- *   - 8 wave64s x 32 queries = 256 queries per workgroup, 64-key tiles,
+ *   - 8 wave64s x 32 queries = 256 queries per workgroup (4 wave64s and
+ *     two workgroups per CU for cross attention over at most 1024 keys),
+ *     64-key tiles,
  *     double-buffered LDS (2 x 32 KiB) with the next tile's global loads in
  *     flight during the current tile's 32 MFMAs per wave.  At 32 queries a
  *     wave needs under 256 registers, so two waves share each SIMD and the
@@ -48,9 +50,9 @@
 #include <string.h>
 #include <type_traits>
 
-/* HK_WAVES 4 (two 128-query workgroups per CU, each with its own barrier)
- * also builds and passes the tests; measured against 8 it was 3% slower on
- * self-attention and 9% faster on 512-key cross-attention, so 8 stays */
+/* 8 waves per workgroup for self-attention; 4-wave workgroups (two
+ * 128-query workgroups per CU, each with its own barrier) were 3% slower
+ * there and serve short cross attention (hk_flash_fwd<..., 4>) */
 #ifndef HK_WAVES
 #define HK_WAVES 8            /* waves per workgroup (two per SIMD) */
 #endif
@@ -154,9 +156,11 @@ hk_rope_keys(const uint16_t *k, const uint64_t *table, uint16_t *out,
     dst[c1] = y;
 }
 
-template <bool SPARSE, bool SPLIT>
-__global__ void __launch_bounds__(HK_THREADS, HK_WG_PER_CU)
+template <bool SPARSE, bool SPLIT, int NW = HK_WAVES>
+__global__ void __launch_bounds__(NW * 64, 8 / NW)
 hk_flash_fwd(hk_attn_args a) {
+    constexpr uint32_t NW_QB = NW * 32;   /* queries per workgroup */
+    constexpr int NW_DMA = 16 / NW;       /* 1-KiB loads per wave, tile and operand */
     extern __shared__ __attribute__((aligned(16))) uint8_t hk_lds[];
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -181,10 +185,11 @@ hk_flash_fwd(hk_attn_args a) {
      * 1-KiB loads, lane l writing physical chunk l & 15 of row 4 i + l / 16;
      * the swizzles are applied on the global side.  (With the RoPE table, K arrives
      * already rotated by hk_rope_keys.) */
-    uint32_t k_dma_off[HK_DMA], v_dma_off[HK_DMA];
+    /* sized for the 4-wave build; the 8-wave one uses the first two */
+    uint32_t k_dma_off[4], v_dma_off[4];
 #pragma unroll
-    for (int i = 0; i < HK_DMA; i++) {
-        const uint32_t row = (wave * HK_DMA + i) * 4u + (lane >> 4);
+    for (int i = 0; i < NW_DMA; i++) {
+        const uint32_t row = (wave * NW_DMA + i) * 4u + (lane >> 4);
         const uint32_t kc = (lane & 15u) ^ (row & 15u);
         const uint32_t vc = (lane & 15u) ^ ((row & 3u) << 2);
         k_dma_off[i] = (row * row_stride + head * HK_HD) * 2u + kc * 16u;
@@ -197,16 +202,16 @@ hk_flash_fwd(hk_attn_args a) {
             hk_attn_rsrc(a.v + base, a.v_bytes - kv0 * row_stride * 2u);
         uint8_t *st = hk_lds + stage * HK_STAGE_BYTES;
 #pragma unroll
-        for (int i = 0; i < HK_DMA; i++)
+        for (int i = 0; i < NW_DMA; i++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 vr, (hk_lds_void *)(st + HK_TILE_BYTES +
-                                    (wave * HK_DMA + i) * 1024u),
+                                    (wave * NW_DMA + i) * 1024u),
                 16, v_dma_off[i], 0, 0, 0);
         const __amdgpu_buffer_rsrc_t kr = hk_attn_rsrc(a.k + base, left);
 #pragma unroll
-        for (int i = 0; i < HK_DMA; i++)
+        for (int i = 0; i < NW_DMA; i++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                kr, (hk_lds_void *)(st + (wave * HK_DMA + i) * 1024u), 16,
+                kr, (hk_lds_void *)(st + (wave * NW_DMA + i) * 1024u), 16,
                 k_dma_off[i], 0, 0, 0);
     };
 
@@ -224,7 +229,7 @@ hk_flash_fwd(hk_attn_args a) {
     /* ---- Q fragments: B operand of S^T = K . Q^T ----
      * k-step ks: Q[q][16 ks + 8 half .. +8]; with the RoPE table, dims d < 48 pair
      * with d + 48, i.e. k-step ks < 3 with ks + 3 in the same lane */
-    const uint32_t qbase = qblock * HK_QB + wave * 32u;
+    const uint32_t qbase = qblock * NW_QB + wave * 32u;
     hk_bf16x8 qf[8];
     {
         const uint32_t q = qbase + col;
@@ -392,10 +397,10 @@ hk_flash_fwd(hk_attn_args a) {
     if (SPARSE) {
         /* 128-row CSR blocks: one per workgroup of 128 queries, two for
          * 256 */
-        const uint32_t qa = qblock * (HK_QB / 128u), qb = qa + 1u;
+        const uint32_t qa = qblock * (NW_QB / 128u), qb = qa + 1u;
         ia = a.sparse_ptr[qa];
         ea = min(a.sparse_ptr[qa + 1], ia + all_tiles);
-        if (HK_QB == 256 && qb < a.sparse_blocks) {
+        if (NW_QB == 256 && qb < a.sparse_blocks) {
             ib = a.sparse_ptr[qb];
             eb = min(a.sparse_ptr[qb + 1], ib + all_tiles);
         }
@@ -412,7 +417,7 @@ hk_flash_fwd(hk_attn_args a) {
             eb = e;
         }
     }
-    const bool first_block = HK_QB == 128 || wave < HK_WAVES / 2;
+    const bool first_block = NW_QB == 128 || wave < NW / 2;
     /* next tile of the sparse schedule: false when done; in_a / in_b say
      * whose list holds it */
     auto advance = [&](uint32_t &tile, bool &in_a, bool &in_b) -> bool {
@@ -641,13 +646,13 @@ hk_flash_fwd(hk_attn_args a) {
                 const float4 v =
                     *(const float4 *)(pw + r * 64u + ((c ^ (r & 15u)) << 2));
                 *(float4 *)(a.part_o +
-                            ((size_t)pid * HK_QB + wave * 32u + r) * HK_HD +
+                            ((size_t)pid * NW_QB + wave * 32u + r) * HK_HD +
                             hd * 64u + c * 4u) = v;
             }
         }
         const float l = l_part + __shfl_xor(l_part, 32, 64);
         if (half == 0)
-            *(float2 *)(a.part_ml + ((size_t)pid * HK_QB + ql) * 2u) =
+            *(float2 *)(a.part_ml + ((size_t)pid * NW_QB + ql) * 2u) =
                 make_float2(m_run, l);
         return;
     }
@@ -730,18 +735,21 @@ __global__ void __launch_bounds__(256) hk_flash_combine(hk_attn_args a) {
  * raised */
 static uint64_t hk_attn_lds_ready = 0;
 
-template <bool SPARSE, bool SPLIT>
+template <bool SPARSE, bool SPLIT, int NW = HK_WAVES>
 static void hk_flash_set_lds() {
     (void)hipFuncSetAttribute(
-        (const void *)hk_flash_fwd<SPARSE, SPLIT>,
+        (const void *)hk_flash_fwd<SPARSE, SPLIT, NW>,
         hipFuncAttributeMaxDynamicSharedMemorySize, HK_ATTN_LDS);
 }
 
 template <bool SPLIT>
 static void hk_flash_launch(struct h3_gpu *gpu, const hk_attn_args &a,
-                            bool masked, uint32_t grid) {
+                            bool masked, uint32_t grid, bool narrow) {
     const dim3 g(grid), b(HK_THREADS);
-    if (masked)
+    if (narrow)
+        hipLaunchKernelGGL((hk_flash_fwd<false, false, 4>), g, dim3(256),
+                           HK_ATTN_LDS, gpu->stream, a);
+    else if (masked)
         hipLaunchKernelGGL((hk_flash_fwd<true, SPLIT>), g, b, HK_ATTN_LDS,
                            gpu->stream, a);
     else
@@ -804,12 +812,21 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
             hk_flash_set_lds<true, false>();
             hk_flash_set_lds<false, true>();
             hk_flash_set_lds<true, true>();
+            hk_flash_set_lds<false, false, 4>();
             hk_attn_lds_ready |= lds_bit;
         }
         hk_attn_args a;
         a.q = q; a.k = k; a.v = v; a.o = o;
         a.q_rows = q_rows; a.kv_rows = kv_rows; a.heads = heads;
-        a.q_blocks = (q_rows + HK_QB - 1) / HK_QB;
+        const bool masked = sparse && gpu->sparse_ptr &&
+                            gpu->sparse_rows == q_rows && q_rows == kv_rows;
+        /* Short cross attention (a text of at most 1024 keys) runs 4-wave,
+         * 128-query workgroups, two per CU: each workgroup walks few key
+         * tiles, so its Q load and O store are a large share of its time,
+         * and the second workgroup's tiles overlap them. */
+        const bool narrow = !masked && q_rows != kv_rows && kv_rows <= 1024;
+        const uint32_t qb_rows = narrow ? 128u : HK_QB;
+        a.q_blocks = (q_rows + qb_rows - 1) / qb_rows;
         a.q_bytes = (uint32_t)q_bytes;
         a.kv_bytes = (uint32_t)kv_bytes;
         a.v_bytes = (uint32_t)v_bytes;
@@ -820,8 +837,6 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
         a.q_eps = q_eps;
         a.scale_log2 = scale * 1.4426950408889634f;
         a.head_major = head_major;
-        const bool masked = sparse && gpu->sparse_ptr &&
-                            gpu->sparse_rows == q_rows && q_rows == kv_rows;
         a.sparse_ptr = masked ? gpu->sparse_ptr : NULL;
         a.sparse_idx = masked ? gpu->sparse_idx : NULL;
         a.sparse_blocks = (q_rows + 127u) / 128u;
@@ -849,7 +864,7 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
                 pieces = s;
             }
         }
-        if (best > 0.6f) pieces = 1;
+        if (best > 0.6f || narrow) pieces = 1;
         /* scratch: the packed RoPE table, the rotated keys, then the split
          * pieces' partials */
         const size_t table_bytes = ((size_t)a.rope_bytes + 255) & ~(size_t)255;
@@ -889,9 +904,9 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
             }
         }
         if (a.full_units)
-            hk_flash_launch<false>(gpu, a, masked, a.full_units);
+            hk_flash_launch<false>(gpu, a, masked, a.full_units, narrow);
         if (pieces > 1) {
-            hk_flash_launch<true>(gpu, a, masked, tail * pieces);
+            hk_flash_launch<true>(gpu, a, masked, tail * pieces, false);
             hipLaunchKernelGGL(hk_flash_combine, dim3(tail * (HK_QB / 8)),
                                dim3(256),
                                0, gpu->stream, a);
