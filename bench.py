@@ -68,8 +68,8 @@ KERNEL_NAMES = {
     "gemm_gelu": "hk_gemm_mfma<2, false> + split tail (FFN up + GELU)",
     "context_kv": "grouped hk_gemm_mfma<0, true>: the text's cross K/V of "
                   "all blocks in one launch",
-    "attention": "hk_flash_fwd<false, false> (self + cross, Q norm "
-                 "(+ RoPE) applied as Q is loaded)",
+    "attention": "hk_flash_fwd<false, false, 8 | 4> (self + cross, Q "
+                 "norm (+ RoPE) applied as Q is loaded)",
     "row_ops": "adaLN / gates / Q-K norm + RoPE / head norm / residual rows",
 }
 

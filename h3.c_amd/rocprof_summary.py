@@ -110,8 +110,9 @@ def traffic(fetch_csv, write_csv, match, calib_elements):
 
 def _groups(path, value="Counter_Value"):
     """(kernel name, grid size, role) -> list of values, in dispatch order.
-    The flash kernel's launches in a forward alternate self / cross
-    attention with one grid size, so they are told apart by order."""
+    Self attention is the 8-wave flash kernel and short cross attention
+    the 4-wave one; traces of the single-instance kernel, whose launches
+    alternate self / cross with one grid size, are told apart by order."""
     rows = []
     for r in csv.DictReader(open(path)):
         grid = (int(r["Grid_Size"]) if "Grid_Size" in r else
@@ -123,7 +124,11 @@ def _groups(path, value="Counter_Value"):
     out = defaultdict(list)
     for _, name, grid, r in rows:
         role = ""
-        if "hk_flash_fwd<false, false" in name:
+        if "hk_flash_fwd<false, false, 4>" in name:
+            role = "cross"
+        elif "hk_flash_fwd<false, false, 8>" in name:
+            role = "self"
+        elif "hk_flash_fwd<false, false>" in name:
             i = seen[(name, grid)]
             seen[(name, grid)] += 1
             role = "self" if i % 2 == 0 else "cross"
