@@ -505,8 +505,15 @@ def h3_denoise(m, video_sigmas, audio_sigmas, reuse_interval,
 
 def wan_block(hidden, context, w, row_map, cos, sin, rows, text_rows, d,
               heads, ffn, hd=128, rope_half=48, eps=1e-6):
-    """One Wan-style block in the op order of the HIP driver
-    (h3.c_amd/host/h3hip_dit.c run_wan_block)."""
+    """One Wan-style block (the benchmark block; the reference has none).
+    Specification, Wan 2.x order: x += slot2 * selfattn(LN(x)(1 + slot1)
+    + slot0); x += crossattn(norm3(x), context) (LayerNorm with affine, no
+    gate); x += slot5 * ffn(LN(x)(1 + slot4) + slot3).  Q/K norms are per
+    head (128-wide weights), as the reference's grouped QK norm is
+    (h3_cuda_attention.cu:175-237).  Primitives: LayerNorm
+    h3_cuda_core.cu:250-295, gate h3_cuda_dit.cu:261-276, GELU-tanh
+    h3_cuda_core.cu:139-158.  The wiring is pinned by the closed-form tests
+    in tests/test_oracle_pins.py (test_wan_block_*)."""
     S = 6
     inner = heads * hd
     scale = 1.0 / math.sqrt(hd)

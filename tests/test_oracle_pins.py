@@ -564,6 +564,215 @@ def test_h3_blocks_fused_adaln_takes_the_next_blocks_weights():
     assert (np.abs(f64(got).reshape(rows, d) - wrong) > tol).any()
 
 
+# ------------------------------------------------- Wan block composition
+#
+# The Wan-style block (BASELINE's benchmark block) has no counterpart in the
+# reference; its specification is the Wan 2.x block order: self-attention on
+# LayerNorm(x)(1 + slot 1) + slot 0 gated by slot 2, cross-attention on
+# norm3(x) (a LayerNorm with its own affine) added without a gate, and the
+# GELU-tanh FFN on LayerNorm(x)(1 + slot 4) + slot 3 gated by slot 5.  Its
+# primitives are the reference's LayerNorm (h3_cuda_core.cu:250-295), gate
+# (h3_cuda_dit.cu:261-276) and GELU-tanh (h3_cuda_core.cu:139-158), each
+# pinned above.  The tests below build weights that reduce one branch of
+# oracle.wan_block to a closed form of its input, with every modulation slot
+# a distinct random value, so that a swapped slot, norm or branch fails.
+
+WAN_EPS = 1e-6
+
+
+def _wan_setup(rows=24, d=256, T=3, text_rows=8, seed=78):
+    r = np.random.default_rng(seed)
+    # a large per-row offset: LayerNorm removes it, a per-head RMS does not
+    x = b(r.standard_normal((rows, d)) + 3.0 * r.standard_normal((rows, 1)))
+    ctx = b(r.standard_normal(text_rows * d))
+    row_map = r.integers(0, 3 * T, rows).astype(np.uint32)
+    ang = r.uniform(-3, 3, rows * 48)
+    return x.ravel(), ctx, row_map, b(np.cos(ang)), b(np.sin(ang))
+
+
+def _wan_wiring_block(d, heads, ffn, T, seed, self_attn=False, cross=False,
+                      ffn_on=False):
+    """Weights of one Wan block (hidden = heads * 128) whose branches are
+    closed forms of their inputs:
+      self_attn: q = k = 0 (uniform softmax), v and out projections the
+        identity, so the branch is the row mean of its adaLN output;
+        otherwise out = 0, so the branch is exactly 0;
+      cross: cq, ck, cv and co projections the identity (no bias), so the
+        branch is SDPA(head_rms(norm3(x)), head_rms(ctx), ctx); otherwise
+        co = 0;
+      ffn_on: fc1 = fc2 = I (ffn = hidden), so the branch is gelu(a) of its
+        adaLN output a; otherwise fc2 = 0.
+    Modulation slots, norm3's weight and bias are distinct random values;
+    every bias not named is 0."""
+    r = np.random.default_rng(seed)
+    hd = 128
+    inner = heads * hd
+    assert inner == d and ffn == d
+    mod = 0.5 * r.standard_normal((T, 3, 6, d))
+    eye = np.eye(d)
+    zero = np.zeros((d, d))
+    qkv = np.concatenate([zero, zero, eye if self_attn else zero])
+    return {
+        "modulation": b(mod.ravel()),
+        "qkv": b(qkv.ravel()), "qkv_bias": b(np.zeros(3 * inner)),
+        "q_norm": b(np.ones(hd)), "k_norm": b(np.ones(hd)),
+        "out": b((eye if self_attn else zero).ravel()),
+        "out_bias": b(np.zeros(d)),
+        "norm3": b(1.0 + 0.5 * r.standard_normal(d)),
+        "norm3_bias": b(0.5 * r.standard_normal(d)),
+        "cq": b(eye.ravel()), "cq_bias": b(np.zeros(inner)),
+        "cq_norm": b(np.ones(hd)),
+        "ck": b(eye.ravel()), "ck_bias": b(np.zeros(inner)),
+        # key rms 2: logits of order 1-2, so p varies over (0.1, 0.9)
+        "ck_norm": b(2.0 * np.ones(hd)),
+        "cv": b(eye.ravel()), "cv_bias": b(np.zeros(inner)),
+        "co": b((eye if cross else zero).ravel()), "co_bias": b(np.zeros(d)),
+        "fc1": b(eye.ravel()), "fc1_bias": b(np.zeros(ffn)),
+        "fc2": b((eye if ffn_on else zero).ravel()),
+        "fc2_bias": b(np.zeros(d)),
+    }
+
+
+def _run_wan(x, ctx, w, row_map, cos, sin, rows, text_rows, d, heads):
+    return oracle.wan_block(x, ctx, w, row_map, cos, sin, rows, text_rows, d,
+                            heads, d, eps=WAN_EPS)
+
+
+def _mod_slot(w, row_map, d, slot):
+    """[rows][d] float64 of modulation slot `slot` at each row's time row."""
+    mod = f64(w["modulation"]).reshape(-1, 6, d)
+    return mod[row_map.astype(np.int64), slot]
+
+
+def test_wan_block_self_attention_branch_wiring():
+    """Self-attention reads LayerNorm(x)(1 + slot 1) + slot 0 (no affine) of
+    the row's own modulation row and is added through gate slot 2.  With
+    q = k = 0 and identity v / out the branch is the row mean y of that
+    adaLN output, so the block returns x + slot2 * y up to the bf16 rounding
+    of y and of the sum; slots 1/0, 3/4, gate slot 5 or norm3's affine in
+    their place fail."""
+    rows, d, heads, T = 24, 256, 2, 3
+    x, ctx, row_map, cos, sin = _wan_setup(rows, d, T)
+    w = _wan_wiring_block(d, heads, d, T, 11, self_attn=True)
+    got = f64(_run_wan(x, ctx, w, row_map, cos, sin, rows, 8, d, heads))
+    got = got.reshape(rows, d)
+
+    def closed(shift, scale, gate_slot, affine=False):
+        a = oracle.layer_adaln(x, w["norm3"] if affine else None,
+                               w["norm3_bias"] if affine else None,
+                               w["modulation"], row_map, rows, d, 6, shift,
+                               scale, WAN_EPS)
+        y = f64(a).reshape(rows, d).mean(axis=0)[None, :]
+        g = _mod_slot(w, row_map, d, gate_slot)
+        return f64(x).reshape(rows, d) + g * y, np.abs(g * y)
+
+    want, gy = closed(0, 1, 2)
+    tol = 2.0 ** -8 * (gy + np.abs(want)) + 1e-30
+    assert (np.abs(got - want) <= tol).all(), float(np.abs(got - want).max())
+    for wrong in ((1, 0, 2), (3, 4, 2), (0, 1, 5), (0, 1, 2, True)):
+        other, _ = closed(*wrong)
+        assert (np.abs(got - other) > tol).any(), wrong
+
+
+def test_wan_block_cross_attention_reads_norm3_and_is_ungated():
+    """Cross-attention's Q projection reads norm3(x) = LayerNorm(x) * w3 + b3
+    (no modulation) and its output is added to the residual without a gate.
+    With identity projections and two text rows, the second all zero, each
+    head's attention is p * v0 with p = sigmoid(scale * q_h . k0_h), q the
+    per-head RMS of norm3(x) and k0 that of the first text row, so the block
+    returns x + p * v0 in closed form (float64 after the pinned primitives,
+    within the bf16 roundings of P, O and the sum).  Q read from x,
+    LayerNorm without the affine, or adaLN slots 0/1, or the residual gated
+    by slot 2 or 5, all fail."""
+    rows, d, heads, T, text = 24, 256, 2, 3, 2
+    hd = 128
+    x, ctx, row_map, cos, sin = _wan_setup(rows, d, T, text_rows=text)
+    ctx = ctx.reshape(text, d).copy()
+    ctx[1] = 0
+    ctx = ctx.ravel()
+    w = _wan_wiring_block(d, heads, d, T, 12, cross=True)
+    got = f64(_run_wan(x, ctx, w, row_map, cos, sin, rows, text, d, heads))
+    got = got.reshape(rows, d)
+    k0 = f64(oracle.head_rms_norm(ctx[:d], w["ck_norm"], 1, heads, hd,
+                                  WAN_EPS)).reshape(heads, hd)
+    v0 = f64(ctx[:d]).reshape(heads, hd)
+    scale = 1.0 / math.sqrt(hd)
+
+    def closed(qin, gate_slot=None):
+        q = f64(oracle.head_rms_norm(qin, w["cq_norm"], rows, heads, hd,
+                                     WAN_EPS)).reshape(rows, heads, hd)
+        p = 1.0 / (1.0 + np.exp(-scale * np.einsum("rhd,hd->rh", q, k0)))
+        o = (p[:, :, None] * v0[None]).reshape(rows, d)
+        if gate_slot is not None:
+            o = o * _mod_slot(w, row_map, d, gate_slot)
+        return f64(x).reshape(rows, d) + o, np.abs(o)
+
+    norm3 = oracle.layer_adaln(x, w["norm3"], w["norm3_bias"], None, None,
+                               rows, d, 6, 0, 0, WAN_EPS)
+    want, o = closed(norm3)
+    tol = 2.0 ** -7 * o + 2.0 ** -8 * np.abs(want) + 1e-30
+    assert (np.abs(got - want) <= tol).all(), float(np.abs(got - want).max())
+    plain_ln = oracle.layer_adaln(x, None, None, None, None, rows, d, 6, 0, 0,
+                                  WAN_EPS)
+    modulated = oracle.layer_adaln(x, None, None, w["modulation"], row_map,
+                                   rows, d, 6, 0, 1, WAN_EPS)
+    for name, other in (("x", closed(x)), ("no affine", closed(plain_ln)),
+                        ("slots 0/1", closed(modulated)),
+                        ("gate 2", closed(norm3, 2)),
+                        ("gate 5", closed(norm3, 5))):
+        assert (np.abs(got - other[0]) > tol).any(), name
+
+
+def test_wan_block_cross_attention_constant_keys_give_mean_of_values():
+    """With the key projection 0 and a constant key bias every text key is
+    the same, so the cross-attention of every row is the mean of the text
+    values, added ungated through co = I: the block returns x + mean(ctx)
+    up to the bf16 rounding of the mean and of the sum, whatever Q is."""
+    rows, d, heads, T, text = 24, 256, 2, 3, 8
+    x, ctx, row_map, cos, sin = _wan_setup(rows, d, T, text_rows=text)
+    w = _wan_wiring_block(d, heads, d, T, 13, cross=True)
+    w["ck"] = b(np.zeros(d * d))
+    w["ck_bias"] = b(np.random.default_rng(5).standard_normal(d))
+    got = f64(_run_wan(x, ctx, w, row_map, cos, sin, rows, text, d, heads))
+    y = f64(ctx).reshape(text, d).mean(axis=0)[None, :]
+    want = f64(x).reshape(rows, d) + y
+    tol = 2.0 ** -8 * (np.abs(y) + np.abs(want))
+    assert (np.abs(got.reshape(rows, d) - want) <= tol).all()
+
+
+def test_wan_block_ffn_branch_wiring():
+    """The FFN reads LayerNorm(x)(1 + slot 4) + slot 3 and is added through
+    gate slot 5.  With the other two branches 0 (bit-exact pass-throughs)
+    and fc1 = fc2 = I the block returns gate(x, gelu(a), slot 5) bit for
+    bit; slots 4/3, 0/1, gate slot 2 or norm3's affine fail."""
+    rows, d, heads, T = 24, 256, 2, 3
+    x, ctx, row_map, cos, sin = _wan_setup(rows, d, T)
+    w = _wan_wiring_block(d, heads, d, T, 14, ffn_on=True)
+    got = _run_wan(x, ctx, w, row_map, cos, sin, rows, 8, d, heads)
+
+    def closed(shift, scale, gate_slot, affine=False):
+        a = oracle.layer_adaln(x, w["norm3"] if affine else None,
+                               w["norm3_bias"] if affine else None,
+                               w["modulation"], row_map, rows, d, 6, shift,
+                               scale, WAN_EPS)
+        return oracle.gate(x, oracle.gelu(a), w["modulation"], row_map, rows,
+                           d, 6, gate_slot)
+
+    np.testing.assert_array_equal(got, closed(3, 4, 5))
+    for wrong in ((4, 3, 5), (0, 1, 5), (3, 4, 2), (3, 4, 5, True)):
+        assert not np.array_equal(got, closed(*wrong)), wrong
+
+
+def test_wan_block_all_branches_off_is_identity():
+    """out = co = fc2 = 0 (zero biases): every branch adds an exact zero, so
+    the block returns its input bit for bit."""
+    rows, d, heads, T = 24, 256, 2, 3
+    x, ctx, row_map, cos, sin = _wan_setup(rows, d, T)
+    w = _wan_wiring_block(d, heads, d, T, 15)
+    got = _run_wan(x, ctx, w, row_map, cos, sin, rows, 8, d, heads)
+    np.testing.assert_array_equal(got, x)
+
+
 def test_rope_rotate_pins():
     """RoPE rotation alone (h3_cuda_attention.cu:218-233): angle 0 is the
     identity, angle pi/2 maps (x, y) to (-y, x) exactly, dims from 96 on are
