@@ -1102,6 +1102,12 @@ static int hk_gemm_bf16_group(struct h3_gpu *gpu, const uint16_t *x,
  * reduction reads them, so the array needs no clearing between calls; calls
  * that overlap on one device share it and race. */
 #define HK_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+/* worst case on MI355X: a split never has more pieces than the 256 CUs,
+ * each an f32 256x256 partial tile (256 KiB), so 256 x 256 KiB = 64 MiB.
+ * Resident on every device the library loads on, called or not. */
+static_assert(HK_NOALLOC_SCRATCH_BYTES ==
+                  (size_t)256 * HK_BM * HK_BN * sizeof(float),
+              "no-alloc scratch sized for 256 CUs of 256x256 f32 partials");
 static __device__ __align__(256) float
     scratch[HK_NOALLOC_SCRATCH_BYTES / sizeof(float)];
 
@@ -1239,6 +1245,12 @@ h3_gpu_tensor *h3_hip_linear_group_table(h3_gpu *gpu,
     h3_gpu_tensor *table = h3_gpu_tensor_from_u32(
         gpu, (const uint32_t *)entries, (size_t)count * 6);
     free(entries);
+    if (table) {
+        table->group_shape[0] = rows;
+        table->group_shape[1] = input_dim;
+        table->group_shape[2] = output_dim;
+        table->group_shape[3] = count;
+    }
     return table;
 }
 
@@ -1246,6 +1258,21 @@ int h3_hip_linear_group_bf16(h3_gpu *gpu, const h3_gpu_tensor *table,
                              uint32_t first, uint32_t count,
                              const h3_gpu_tensor *input, uint32_t rows,
                              uint32_t input_dim, uint32_t output_dim) {
+    /* the table's addresses were validated for one shape: running them at
+     * another would read and write past the problems' tensors */
+    if (table && table->group_shape[3] == 0)
+        return hk_fail(gpu, "grouped linear: the table was not built by "
+                            "h3_hip_linear_group_table");
+    if (table && (rows != table->group_shape[0] || input_dim != table->group_shape[1] ||
+        output_dim != table->group_shape[2]))
+        return hk_fail(gpu, "grouped linear: shape %ux%ux%u differs from the "
+                            "table's %ux%ux%u", rows, input_dim, output_dim,
+                       table->group_shape[0], table->group_shape[1],
+                       table->group_shape[2]);
+    if (table && (uint64_t)first + count > table->group_shape[3])
+        return hk_fail(gpu, "grouped linear: problems [%u, %u) past the "
+                            "table's %u", first, first + count,
+                       table->group_shape[3]);
     if (!hk_require(gpu, table, ((size_t)first + count) * 6, H3_GPU_U32,
                     "grouped linear table") ||
         !hk_require(gpu, input, (size_t)rows * input_dim, H3_GPU_BF16,

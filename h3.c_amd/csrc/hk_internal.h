@@ -25,6 +25,10 @@ struct h3_gpu_tensor {
     size_t bytes;
     h3_gpu_dtype dtype;
     struct h3_gpu *owner;
+    /* host-side record of a grouped-linear table: the (rows, input_dim,
+     * output_dim, problems) it was built and validated for; all zero for
+     * every other tensor */
+    uint32_t group_shape[4];
 };
 
 struct hk_cache_block;

@@ -171,7 +171,10 @@ int h3_gpu_gate_layer_adaln_bf16(
  * h3_hip_linear_group_table builds holds the problems' device addresses
  * (free it with h3_gpu_tensor_free; it stays valid while the tensors
  * live), and h3_hip_linear_group_bf16 runs problems [first, first + count)
- * of it on `input`.  Tensors must meet the MFMA kernel's alignment (16-byte
+ * of it on `input`, with the rows, input_dim and output_dim the table was
+ * built with (another shape, or problems past the table's count, fail with
+ * an error: the table's addresses were validated for that shape only).
+ * Tensors must meet the MFMA kernel's alignment (16-byte
  * weights, 8-byte outputs and biases), which the table checks.  Each
  * output is exactly what h3_gpu_linear_bf16 computes with the data-
  * parallel kernel.  Biases may be NULL (or the array NULL).  No reference
@@ -210,9 +213,13 @@ int h3_hip_linear_pair_bf16(h3_gpu *gpu, h3_gpu_tensor *output0,
  * 256x256 tiles would leave over half the CUs idle) in a static 64 MiB
  * device array per GPU instead of the context's on-demand scratch.  A
  * launch whose split would need more fails with an error naming the size.
- * Calls that overlap on one GPU share that array and race.  No counterpart
- * in the reference: it is for callers that cannot allocate device memory
- * (HIP graph capture, fixed-footprint serving loops). */
+ * The array (256 CUs x one 256x256 f32 tile) is resident on every GPU the
+ * library loads on, whether or not this entry is called.  Calls that
+ * overlap on one GPU share that array and race.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory
+ * (fixed-footprint serving loops, harnesses that forbid hipMalloc); it
+ * makes no device allocation, but recording it into a HIP graph is not
+ * tested. */
 int h3_hip_linear_bf16_noalloc(h3_gpu *gpu, h3_gpu_tensor *output,
                                const h3_gpu_tensor *input,
                                const h3_gpu_tensor *weight,

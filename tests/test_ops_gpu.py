@@ -140,6 +140,43 @@ def test_linear_group(gpu, m, k, n, count, first, exact):
         gpu.L.h3_gpu_tensor_free(table)
 
 
+def test_linear_group_rejects_another_shape(gpu):
+    """The table's addresses were validated for the shape it was built with:
+    a launch with more rows, another width, problems past the table's count
+    or a tensor that is not a table fails before any kernel runs, and the
+    outputs are left alone."""
+    m, k, n = 128, 256, 256
+    rng = np.random.default_rng(31)
+    tx = gpu.bf16(rand_bf16(rng, 2 * m * 2 * k))
+    tws = [gpu.bf16(rand_bf16(rng, n * k, 0.05)) for _ in range(2)]
+    tos = [gpu.new_bf16(m * n) for _ in range(2)]
+    for t in tos:
+        gpu.run("h3_gpu_fill_normal_bf16", t, 0, m * n, 3, 0.0, 1.0)
+    before = [gpu.read_bf16(t).view(np.uint16).copy() for t in tos]
+    P = C.c_void_p
+    table = gpu.L.h3_hip_linear_group_table(
+        gpu.h, (P * 2)(*tos), (P * 2)(*tws), None, 2, m, k, n)
+    assert table, gpu.error()
+    plain = gpu.L.h3_gpu_tensor_from_u32(
+        gpu.h, np.zeros(12, np.uint32).ctypes.data_as(P), 12)
+    assert plain, gpu.error()
+    try:
+        for args, what in (((0, 2, tx, 2 * m, k, n), "differs"),
+                           ((0, 2, tx, m, 2 * k, n), "differs"),
+                           ((0, 2, tx, m, k, 2 * n), "differs"),
+                           ((1, 2, tx, m, k, n), "past the"),
+                           ((0, 2, tx, m, k, n), "not built")):
+            tab = plain if what == "not built" else table
+            with pytest.raises(RuntimeError, match=what):
+                gpu.run("h3_hip_linear_group_bf16", tab, *args)
+        for t, old in zip(tos, before):
+            assert np.array_equal(gpu.read_bf16(t).view(np.uint16), old)
+        gpu.run("h3_hip_linear_group_bf16", table, 0, 2, tx, m, k, n)
+    finally:
+        gpu.L.h3_gpu_tensor_free(table)
+        gpu.L.h3_gpu_tensor_free(plain)
+
+
 def test_linear_stats_kind(gpu):
     """Routing-shape rule of the stats counters (reference
     h3_cuda_core.cu:838-841): rows >= 32, in >= 256, out >= 256 -> kind 1."""
