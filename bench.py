@@ -140,6 +140,35 @@ def profile_pass(gpu, dit, blocks):
     log("profile pass done")
 
 
+def measured_peak(gpu, iterations=100000, reps=3):
+    """The bf16 MFMA rate this GPU sustains with MFMAs alone
+    (h3_hip_mfma_loop: one workgroup of four waves per CU, the GEMM's
+    occupancy, 16 independent 32x32x16 MFMAs per iteration from registers,
+    no LDS or memory traffic), timed by HIP events; the fastest of `reps`
+    launches of about 20 ms each."""
+    import ctypes as C
+    L = gpu.L
+    sink = gpu.new_f32(1024 * 256)
+    flops = C.c_double()
+    best = None
+    gpu.begin()
+    gpu.check(L.h3_hip_mfma_loop(gpu.h, sink, 1000, C.byref(flops)), "warm")
+    gpu.submit()
+    for _ in range(reps):
+        gpu.begin()
+        L.h3_hip_marker(gpu.h, 4)
+        gpu.check(L.h3_hip_mfma_loop(gpu.h, sink, iterations, C.byref(flops)),
+                  "mfma loop")
+        L.h3_hip_marker(gpu.h, 5)
+        gpu.submit()
+        ms = C.c_double()
+        L.h3_hip_marker_elapsed(gpu.h, 4, 5, C.byref(ms))
+        tf = flops.value / (ms.value / 1e3) / 1e12
+        best = tf if best is None else max(best, tf)
+    gpu.free(sink)
+    return best
+
+
 def h3_measure(gpu, blocks, reps, latent_h=32, latent_w=32, full=True):
     """The H3 block at a real shape (512 text + 74 audio + video rows of a
     22-frame latent_h x latent_w latent: 2378 rows at 512x512, 3421 at
@@ -203,7 +232,41 @@ def h3_measure(gpu, blocks, reps, latent_h=32, latent_w=32, full=True):
         hflops = hdit.block_flops()
         real = {"rows": int(n), "s_per_forward": round(hms / 1e3, 4),
                 "ms_per_block": round(hms / blocks, 3),
-                "tflops": round(blocks * hflops / (hms / 1e3) / 1e12, 1)}
+                "tflops": round(blocks * hflops / (hms / 1e3) / 1e12, 1),
+                "frac_of_peak": round(blocks * hflops / (hms / 1e3) / 1e12 /
+                                      BF16_PEAK_TFLOPS, 4)}
+        # per-class replays at this shape, as for the Wan forward
+        cref = C.byref(hcfg)
+        kern = {}
+        for cname, mask, what in (
+                ("gemm_plain", OPS_GEMM, "QKV + out-projection "
+                 "(hk_gemm_mfma<0>, split tails)"),
+                ("mlp_swiglu", OPS_ACT, "fc1 with SwiGLU epilogue "
+                 "(hk_gemm_mfma<1>) + fc2 (hk_gemm_mfma<0>)"),
+                ("attention", OPS_ATTN, "hk_flash_fwd (joint self-"
+                 "attention, key-split last round)"),
+                ("row_ops", OPS_ROWS, "adaLN / gate+adaLN / grouped Q-K "
+                 "norm + RoPE rows")):
+            cms = class_replay(gpu, hdit, blocks, mask)
+            fl = L.h3hip_dit_block_class_flops(cref, mask)
+            kern[cname] = {"kernel": what, "ms_per_forward": round(cms, 3)}
+            if fl:
+                tf = blocks * fl / (cms / 1e3) / 1e12
+                kern[cname].update(tflops=round(tf, 1),
+                                   frac_of_peak=round(tf / BF16_PEAK_TFLOPS,
+                                                      4))
+        real["kernels"] = kern
+        gfl = (L.h3hip_dit_block_class_flops(cref, OPS_GEMM) +
+               L.h3hip_dit_block_class_flops(cref, OPS_ACT))
+        gms = kern["gemm_plain"]["ms_per_forward"] + \
+            kern["mlp_swiglu"]["ms_per_forward"]
+        gtf = blocks * gfl / (gms / 1e3) / 1e12
+        real["roofline"] = {
+            "kernel": "the block's GEMMs (QKV, out, fc1 SwiGLU, fc2)",
+            "bound": "mfma", "achieved": round(gtf, 1),
+            "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(gtf / BF16_PEAK_TFLOPS, 4),
+            "flops_per_block": gfl}
         if not full:
             return real, None
         # the reference's documented block-sparse window (README H3_SPARSE_ATTN
@@ -342,10 +405,14 @@ def wan_864x480(gpu, blocks, reps):
 
 
 def weight_load(size_gib=2.0):
-    """File -> HBM throughput of h3_gpu_tensor_load_bf16 on a freshly
-    written file (so mostly page-cache resident): O_DIRECT and buffered
-    reads, against read-everything-then-upload (h3_gpu_tensor_from_bf16 of
-    an np.fromfile array), the reference's load order."""
+    """File -> HBM throughput of h3_gpu_tensor_load_bf16 (the pipelined
+    loader), O_DIRECT and buffered, against read-everything-then-upload
+    (np.fromfile, then h3_gpu_tensor_from_bf16: the reference's load
+    order), each with the file's pages evicted from the page cache first
+    ("cold": fsync, then posix_fadvise(DONTNEED) before every repetition, so
+    the bytes come from the disk) and, for the buffered legs, with the file
+    read once just before ("hot": page-cache resident).  Best of 3 per leg.
+    O_DIRECT bypasses the page cache, so it has one leg."""
     import shutil
     import tempfile
     n = int(size_gib * (1 << 30)) // 2
@@ -357,26 +424,57 @@ def weight_load(size_gib=2.0):
             f.write(b"\0" * 4096)
             np.random.default_rng(0).integers(
                 0, 1 << 16, n, dtype=np.uint16).tofile(f)
+            f.flush()
+            os.fsync(f.fileno())
+
+        def evict():
+            fd = os.open(path, os.O_RDONLY)
+            try:
+                os.fsync(fd)
+                os.posix_fadvise(fd, 0, 0, os.POSIX_FADV_DONTNEED)
+            finally:
+                os.close(fd)
+
+        def warm():
+            with open(path, "rb") as f:
+                while f.read(64 << 20):
+                    pass
+
         gpu = h3hip.Gpu()
         try:
-            for mode, env in (("direct", "1"), ("buffered", "0")):
-                os.environ["H3_HIP_DIRECT_IO"] = env
+            def loader():
+                t = gpu.load(path, 4096, n)
+                gpu.free(t)
+
+            def read_upload():
+                a = np.fromfile(path, dtype=np.uint16, offset=4096)
+                t = gpu.bf16(a)
+                gpu.free(t)
+
+            legs = (("direct_gb_s", "1", loader, evict),
+                    ("buffered_cold_gb_s", "0", loader, evict),
+                    ("buffered_hot_gb_s", "0", loader, warm),
+                    ("read_then_upload_cold_gb_s", None, read_upload, evict),
+                    ("read_then_upload_hot_gb_s", None, read_upload, warm))
+            for key, env, fn, prep in legs:
+                if env is None:
+                    os.environ.pop("H3_HIP_DIRECT_IO", None)
+                else:
+                    os.environ["H3_HIP_DIRECT_IO"] = env
                 best = None
                 for _ in range(3):
+                    prep()
                     t0 = time.perf_counter()
-                    t = gpu.load(path, 4096, n)
+                    fn()
                     dt = time.perf_counter() - t0
-                    gpu.free(t)
                     best = dt if best is None else min(best, dt)
-                out[mode + "_gb_s"] = round(2 * n / best / 1e9, 2)
+                out[key] = round(2 * n / best / 1e9, 2)
             os.environ.pop("H3_HIP_DIRECT_IO", None)
-            t0 = time.perf_counter()
-            a = np.fromfile(path, dtype=np.uint16, offset=4096)
-            t = gpu.bf16(a)
-            dt = time.perf_counter() - t0
-            gpu.free(t)
-            del a
-            out["read_then_upload_gb_s"] = round(2 * n / dt / 1e9, 2)
+            out["cache_state"] = (
+                "cold: fsync + posix_fadvise(DONTNEED) before each "
+                "repetition (bytes from the disk); hot: the file read once "
+                "just before (page-cache resident); O_DIRECT bypasses the "
+                "page cache")
         finally:
             gpu.close()
     finally:
@@ -534,6 +632,8 @@ def main():
     per_launch_flops = plain_flops / plain_launches
     per_launch_ms = gemm_ms / (blocks * plain_launches)
     dit.close()
+    log("measured MFMA peak ...")
+    peak_meas = measured_peak(gpu)
 
     sweep = wan_big = loading = None
     if not args.no_extras:
@@ -608,6 +708,15 @@ def main():
                      "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(per_launch_flops / (per_launch_ms / 1e3) /
                                    1e12 / BF16_PEAK_TFLOPS, 4),
+                     "peak_measured": round(peak_meas, 1),
+                     "frac_of_measured": round(
+                         per_launch_flops / (per_launch_ms / 1e3) / 1e12 /
+                         peak_meas, 4),
+                     "peak_measured_how": "h3_hip_mfma_loop: 4 waves per "
+                                          "CU, 16 independent 32x32x16 bf16 "
+                                          "MFMAs per iteration from "
+                                          "registers, no LDS or memory; "
+                                          "fastest of 3 x ~20 ms, HIP events",
                      "flops_per_launch": per_launch_flops,
                      "avg_launch_us": round(per_launch_ms * 1e3, 1),
                      "traffic": load_traffic("gemm_plain_wan512_traffic.json")},

@@ -161,6 +161,41 @@ __device__ __forceinline__ void hk_tile_coords(uint32_t tile, uint32_t tiles_m,
     tile_n = in_band / band_rows;
 }
 
+/* Phase trace of the MFMA GEMM (built only with -DHK_GEMM_TRACE, the
+ * `make trace` library; the product build compiles none of it).  Thread 0
+ * of each workgroup records the constant 100 MHz real-time counter at the
+ * phase boundaries of each of its tiles, and the shader-clock counter at a
+ * tile's start and end:
+ *   0 tile start          1 first stage landed (prologue done)
+ *   2 main loop done      3 bias loaded, LDS free (epilogue start)
+ *   4 tile staged in LDS  5 global stores issued
+ *   6 tile end (LDS reads done, barrier)
+ *   7 the tile's index in the launch
+ *   8 / 9 shader clock at 0 / 6
+ * h3_hip_gemm_trace_clear / _read (trace build only) reset and fetch it. */
+#ifdef HK_GEMM_TRACE
+#define HK_TRACE_WG 1024u
+#define HK_TRACE_ITERS 16u
+#define HK_TRACE_SLOTS 10u
+static __device__ uint64_t
+    hk_gemm_trace[HK_TRACE_WG * HK_TRACE_ITERS * HK_TRACE_SLOTS];
+__device__ __forceinline__ void hk_trace_put(uint32_t iter, uint32_t slot,
+                                             uint64_t value) {
+    if (threadIdx.x == 0 && blockIdx.x < HK_TRACE_WG && iter < HK_TRACE_ITERS)
+        hk_gemm_trace[(blockIdx.x * HK_TRACE_ITERS + iter) * HK_TRACE_SLOTS +
+                      slot] = value;
+}
+#define HK_TRACE(p) \
+    hk_trace_put(iter, (p), __builtin_amdgcn_s_memrealtime())
+#define HK_TRACE_CLOCK(p) \
+    hk_trace_put(iter, (p), __builtin_amdgcn_s_memtime())
+#define HK_TRACE_VALUE(p, v) hk_trace_put(iter, (p), (v))
+#else
+#define HK_TRACE(p) ((void)0)
+#define HK_TRACE_CLOCK(p) ((void)0)
+#define HK_TRACE_VALUE(p, v) ((void)0)
+#endif
+
 template <int EPI, bool GROUP = false>
 __global__ void __launch_bounds__(HK_GEMM_THREADS, 1)
 __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -182,7 +217,10 @@ hk_gemm_mfma(hk_gemm_args g) {
     uint32_t slot = blockIdx.x;
     if ((nwg & 7u) == 0) slot = (slot & 7u) * (nwg >> 3) + (slot >> 3);
     const uint32_t tile_count = partial ? nwg : g.tile_count;
+    uint32_t iter = 0;
+    (void)iter;
     for (uint32_t item = slot; item < tile_count; item += nwg) {
+
     /* Everything lane-dependent is recomputed per tile: laundering the
      * thread index keeps the compiler from hoisting those values out of the
      * tile loop, where they would stay live through the epilogue (which
@@ -191,6 +229,9 @@ hk_gemm_mfma(hk_gemm_args g) {
     uint32_t tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
     const uint32_t lane = tid & 63;
+    HK_TRACE(0);
+    HK_TRACE_CLOCK(8);
+    HK_TRACE_VALUE(7, item);
     uint32_t pid = item;
     uint32_t k_first = 0, split = 0, part = 0;
     const uint16_t *wsrc = g.w;
@@ -365,6 +406,7 @@ hk_gemm_mfma(hk_gemm_args g) {
     issue_loads(0, 0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    HK_TRACE(1);
     if (k_steps > 1) issue_loads(1, HK_BK);
     read_frags(0, 0, 0);
     wait_frags(0);
@@ -393,6 +435,7 @@ hk_gemm_mfma(hk_gemm_args g) {
         wait_frags(0);
     }
 #undef HK_PIN
+    HK_TRACE(2);
 
     /* ---- epilogue ----
      * acc[i][j][r] = C[m][n] with
@@ -456,6 +499,7 @@ hk_gemm_mfma(hk_gemm_args g) {
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    HK_TRACE(3);
     auto lds_put = [&](uint32_t row, uint32_t col, uint2 v) {
         const uint32_t chunk = (col >> 3) ^ (row & (chunks - 1u));
         *(uint2 *)(hk_smem + row * pitch + chunk * 16u + (col & 7u) * 2u) = v;
@@ -508,6 +552,7 @@ hk_gemm_mfma(hk_gemm_args g) {
         }
     }
     __syncthreads();
+    HK_TRACE(4);
     /* rows leave 16 bytes per lane; N % 4 == 0, so a chunk is either whole,
      * its first 8 bytes, or past the end.  Whole chunks are nontemporal
      * stores: every CU writes its tile at about the same moment, and
@@ -539,12 +584,33 @@ hk_gemm_mfma(hk_gemm_args g) {
                 *(uint2 *)dst = make_uint2(v[u].x, v[u].y);
         }
     }
+    HK_TRACE(5);
     /* the next tile's loads overwrite this tile's staged rows: every wave
      * must be done reading them (the stores may still be in flight) */
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
+    HK_TRACE(6);
+    HK_TRACE_CLOCK(9);
+    iter++;
     } /* tiles */
 }
+
+#ifdef HK_GEMM_TRACE
+extern "C" int h3_hip_gemm_trace_clear(void) {
+    static uint64_t zeros[HK_TRACE_WG * HK_TRACE_ITERS * HK_TRACE_SLOTS];
+    return hipMemcpyToSymbol(HIP_SYMBOL(hk_gemm_trace), zeros,
+                             sizeof(zeros)) == hipSuccess;
+}
+
+/* copies the trace, [workgroup][tile iteration][slot] u64, to `out`
+ * (HK_TRACE_WG x HK_TRACE_ITERS x HK_TRACE_SLOTS entries) */
+extern "C" int h3_hip_gemm_trace_read(uint64_t *out, size_t entries) {
+    if (entries < (size_t)HK_TRACE_WG * HK_TRACE_ITERS * HK_TRACE_SLOTS)
+        return 0;
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(hk_gemm_trace),
+                               sizeof(hk_gemm_trace)) == hipSuccess;
+}
+#endif
 
 /* Skinny GEMM for M <= 64 rows (the per-block modulation projections:
  * time rows x 2688 against 96768 x 2688 weights).  Bound by streaming W
@@ -751,8 +817,8 @@ hk_splitk_reduce(hk_gemm_args g, uint32_t splits) {
         const uint32_t row = (blockIdx.x & 31u) * 8u + (threadIdx.x >> 5);
         const uint32_t c4 = (threadIdx.x & 31u) * 4u;
         uint32_t tile_m, tile_n;
-        hk_tile_coords(g.tile_base + part, g.tiles_m, g.tiles_n, tile_m,
-                       tile_n);
+        hk_tile_coords(g.tile_base + part, g.tiles_m, g.tiles_n,
+                       tile_m, tile_n);
         const uint32_t m = tile_m * HK_BM + row, n = tile_n * 128u + c4;
         if (m >= g.m || n >= g.n) return;
         const size_t stride = (size_t)g.part_tiles * (HK_BM * HK_BN);
@@ -1474,3 +1540,63 @@ int h3_gpu_grouped_qkv_linear_rope_bf16(
 }
 
 } /* extern "C" */
+
+/* The bf16 MFMA rate this GPU sustains with nothing else running: every CU
+ * runs one workgroup of four waves (one per SIMD, the GEMM's occupancy),
+ * each issuing v_mfma_f32_32x32x16_bf16 back to back into the 16
+ * accumulators of the GEMM's 128x128 wave tile, operands held in
+ * registers (no LDS, no memory).  The measured ceiling next to the vendor
+ * peak; the sums go to `sink` so that nothing is folded away. */
+__global__ void __launch_bounds__(HK_GEMM_THREADS, 1)
+__attribute__((amdgpu_waves_per_eu(1, 1)))
+hk_mfma_loop(float *sink, uint32_t iterations) {
+    hk_f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+    hk_bf16x8 fa[4], fb[4];
+    const uint32_t lane = threadIdx.x & 63u;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            /* small values of the order 2^-7: sums stay finite */
+            fa[i][e] = (__bf16)(0.0078125f * (float)((lane + i + e) & 7u));
+            fb[i][e] = (__bf16)(0.0078125f * (float)((lane * 3u + i + e) & 7u));
+        }
+    for (uint32_t it = 0; it < iterations; it++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+    float total = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) total += acc[i][j][r];
+    sink[blockIdx.x * HK_GEMM_THREADS + threadIdx.x] = total;
+}
+
+extern "C" int h3_hip_mfma_loop(h3_gpu *gpu, h3_gpu_tensor *sink,
+                                uint32_t iterations, double *flops) {
+    if (!hk_require_active(gpu)) return 0;
+    const uint32_t cus = gpu->num_cus > 0 ? (uint32_t)gpu->num_cus : 256u;
+    if (!hk_require(gpu, sink, (size_t)cus * HK_GEMM_THREADS, H3_GPU_F32,
+                    "MFMA loop sink"))
+        return 0;
+    hk_op_begin(gpu, "mfma_loop");
+    hipLaunchKernelGGL(hk_mfma_loop, dim3(cus), dim3(HK_GEMM_THREADS), 0,
+                       gpu->stream, (float *)sink->data, iterations);
+    /* 16 MFMAs of 32 x 32 x 16 (2 flops each) per iteration and wave */
+    if (flops)
+        *flops = (double)cus * 4.0 * iterations * 16.0 * 2.0 * 32 * 32 * 16;
+    return hk_op_end(gpu, "mfma_loop", 0);
+}

@@ -189,6 +189,7 @@ def lib():
                                        C.POINTER(C.c_double)]),
         "h3_hip_op_timing_names": (_I, [_P, C.c_char_p, _SZ]),
         "h3_hip_marker": (_I, [_P, _I]),
+        "h3_hip_mfma_loop": (_I, [_P, _P, _U32, C.POINTER(C.c_double)]),
         "h3_hip_marker_elapsed": (_I, [_P, _I, _I, C.POINTER(C.c_double)]),
         # DiT driver
         "h3hip_dit_create": (_P, [_P, C.POINTER(DitConfig), C.c_char_p, _SZ]),
@@ -293,6 +294,15 @@ def lib():
         fn.restype = res
         fn.argtypes = args
         setattr(ns, name, fn)
+    # the GEMM phase-trace build's extra entry points (make trace)
+    for name, (res, args) in {
+            "h3_hip_gemm_trace_clear": (_I, []),
+            "h3_hip_gemm_trace_read": (_I, [_P, _SZ])}.items():
+        if hasattr(L, name):
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+            setattr(ns, name, fn)
     _lib = ns
     return ns
 

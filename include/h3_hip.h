@@ -287,6 +287,15 @@ int h3_hip_op_timing_read(h3_gpu *gpu, const char *prefix,
 /* Names of the distinct timed ops, '\n'-separated, into buffer. */
 int h3_hip_op_timing_names(h3_gpu *gpu, char *buffer, size_t buffer_size);
 
+/* Launches the measured-peak kernel: one workgroup of four waves per CU,
+ * each wave issuing `iterations` x 16 bf16 MFMAs (32x32x16) from registers
+ * with no LDS or memory traffic; `sink` (F32, at least CUs x 256
+ * elements) receives the sums.  *flops is the launch's FLOP count, so a
+ * caller timing it between two markers gets the sustained MFMA rate.  No
+ * reference counterpart: the benchmark reports it beside the vendor peak. */
+int h3_hip_mfma_loop(h3_gpu *gpu, h3_gpu_tensor *sink, uint32_t iterations,
+                     double *flops);
+
 /* Device milliseconds between two markers recorded on the context stream. */
 int h3_hip_marker(h3_gpu *gpu, int slot);
 int h3_hip_marker_elapsed(h3_gpu *gpu, int from_slot, int to_slot,

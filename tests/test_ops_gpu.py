@@ -177,6 +177,32 @@ def test_linear_group_rejects_another_shape(gpu):
         gpu.L.h3_gpu_tensor_free(plain)
 
 
+def test_mfma_loop_measures_a_plausible_rate(gpu):
+    """h3_hip_mfma_loop (the bench's measured MFMA ceiling): the sums are
+    exact small multiples of 2^-14, so two iterations give exactly twice
+    one iteration's sums; the FLOP count it reports over the event time is
+    a rate between 20% and 120% of the 2.5 PFLOP/s bf16 peak."""
+    # room for up to 1024 CUs; entries of CUs the GPU lacks stay 0
+    sink = gpu.f32(np.zeros(1024 * 256, np.float32))
+    flops = C.c_double()
+    got = []
+    for it in (1, 2):
+        gpu.run("h3_hip_mfma_loop", sink, it, C.byref(flops))
+        got.append(gpu.read_f32(sink))
+    assert np.isfinite(got[0]).all() and (got[0] >= 0).all()
+    assert got[0].max() > 0
+    np.testing.assert_array_equal(got[1], 2 * got[0])
+    gpu.begin()
+    gpu.L.h3_hip_marker(gpu.h, 0)
+    assert gpu.L.h3_hip_mfma_loop(gpu.h, sink, 20000, C.byref(flops))
+    gpu.L.h3_hip_marker(gpu.h, 1)
+    gpu.submit()
+    ms = C.c_double()
+    assert gpu.L.h3_hip_marker_elapsed(gpu.h, 0, 1, C.byref(ms))
+    tflops = flops.value / (ms.value * 1e-3) / 1e12
+    assert 500 < tflops < 3000, tflops
+
+
 def test_linear_stats_kind(gpu):
     """Routing-shape rule of the stats counters (reference
     h3_cuda_core.cu:838-841): rows >= 32, in >= 256, out >= 256 -> kind 1."""
