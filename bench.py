@@ -169,6 +169,42 @@ def measured_peak(gpu, iterations=100000, reps=3):
     return best
 
 
+def hbm_roof(gpu, mib=1024, reps=10):
+    """The HBM rates plain streaming reaches on this GPU, for the row
+    kernels' bytes to be read against: a device-to-device copy
+    (hipMemcpyAsync through h3_gpu_copy_bf16) and this library's add_bf16
+    (two reads, one write, 16 bytes per lane), over `mib` MiB operands,
+    HIP events around `reps` launches after two warm-ups."""
+    import ctypes as C
+    L = gpu.L
+    n = mib * (1 << 20) // 2
+    a, b, c = gpu.new_bf16(n), gpu.new_bf16(n), gpu.new_bf16(n)
+    gpu.begin()
+    L.h3_gpu_fill_normal_bf16(gpu.h, a, 0, n, 5, 0.0, 1.0)
+    L.h3_gpu_fill_normal_bf16(gpu.h, b, 0, n, 6, 0.0, 1.0)
+    gpu.submit()
+    out = {"operand_mib": mib}
+    for key, launch, moved in (
+            ("copy_gb_s", lambda: L.h3_gpu_copy_bf16(gpu.h, c, 0, a, 0, n),
+             4 * n),
+            ("add_bf16_gb_s", lambda: L.h3_gpu_add_bf16(gpu.h, c, a, b, n),
+             6 * n)):
+        gpu.begin()
+        for _ in range(2):
+            gpu.check(launch(), key)
+        L.h3_hip_marker(gpu.h, 8)
+        for _ in range(reps):
+            gpu.check(launch(), key)
+        L.h3_hip_marker(gpu.h, 9)
+        gpu.submit()
+        ms = C.c_double()
+        L.h3_hip_marker_elapsed(gpu.h, 8, 9, C.byref(ms))
+        out[key] = round(moved / (ms.value / reps / 1e3) / 1e9, 1)
+    for t in (a, b, c):
+        gpu.free(t)
+    return out
+
+
 def h3_measure(gpu, blocks, reps, latent_h=32, latent_w=32, full=True):
     """The H3 block at a real shape (512 text + 74 audio + video rows of a
     22-frame latent_h x latent_w latent: 2378 rows at 512x512, 3421 at
@@ -582,6 +618,12 @@ def main():
                          "plain GEMMs, one 64 Mi-element copy-like kernel of "
                          "known traffic (add_bf16) as the counter "
                          "calibration; no timing line")
+    ap.add_argument("--h3-only", action="store_true",
+                    help="for rocprofv3 runs: only the H3 block at its real "
+                         "shape (2378 rows, 50 blocks): the forward, its "
+                         "per-class replays, then add_bf16 over 64 Mi "
+                         "elements as the counter calibration; prints that "
+                         "section's JSON, not the bench line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this backend runs on one GPU; the "
@@ -593,6 +635,18 @@ def main():
 
     gpu = h3hip.Gpu()
     blocks = args.blocks
+    if args.h3_only:
+        real, _ = h3_measure(gpu, blocks, max(2, args.steps // 2), full=False)
+        n = 64 << 20
+        a, b, c = gpu.new_bf16(n), gpu.new_bf16(n), gpu.new_bf16(n)
+        gpu.begin()
+        gpu.L.h3_gpu_fill_normal_bf16(gpu.h, a, 0, n, 5, 0.0, 1.0)
+        gpu.L.h3_gpu_fill_normal_bf16(gpu.h, b, 0, n, 6, 0.0, 1.0)
+        gpu.check(gpu.L.h3_gpu_add_bf16(gpu.h, c, a, b, n), "calibration")
+        gpu.submit()
+        gpu.close()
+        print(json.dumps({"h3_real_shape": real}), flush=True)
+        return
     # ---- BASELINE shape: Wan block, 512x512x22f -> 6 x 32 x 32 tokens
     rows, text = 6 * 32 * 32, 512
     cfg = h3hip.dit_config(h3hip.FAMILY_WAN, 5120, 40, 13824, rows,
@@ -632,8 +686,9 @@ def main():
     per_launch_flops = plain_flops / plain_launches
     per_launch_ms = gemm_ms / (blocks * plain_launches)
     dit.close()
-    log("measured MFMA peak ...")
+    log("measured MFMA peak and HBM streaming rates ...")
     peak_meas = measured_peak(gpu)
+    hbm = hbm_roof(gpu)
 
     sweep = wan_big = loading = None
     if not args.no_extras:
@@ -720,6 +775,9 @@ def main():
                      "flops_per_launch": per_launch_flops,
                      "avg_launch_us": round(per_launch_ms * 1e3, 1),
                      "traffic": load_traffic("gemm_plain_wan512_traffic.json")},
+        "hbm_streaming": dict(hbm, note="practical HBM rates on this GPU "
+                                         "(vendor peak 8000 GB/s), for the "
+                                         "row kernels' GB/s in profiles/"),
         "h3_real_shape": h3_real,
         "h3_864x480": h3_big,
         "denoise": denoise,

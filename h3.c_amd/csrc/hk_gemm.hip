@@ -887,7 +887,10 @@ static uint32_t hk_gemm_grid(uint32_t tiles, uint32_t cus) {
         const char *e = getenv("H3_HIP_GEMM_PERSIST");
         persist = e ? atoi(e) : 1;
     }
-    if (!persist || tiles <= cus) return tiles;
+    /* a multiple of 8 workgroups, so that the kernel's XCD regroup applies
+     * (each XCD a contiguous run of tiles sharing its L2); the few extra
+     * workgroups of a one-round launch find no tile and exit */
+    if (!persist || tiles <= cus) return (tiles + 7u) & ~7u;
     const uint32_t rounds = (tiles + cus - 1) / cus;
     const uint32_t wgs = ((tiles + rounds - 1) / rounds + 7u) & ~7u;
     return wgs < cus ? wgs : cus;

@@ -861,14 +861,13 @@ hk_head_rms_kernel(uint16_t *tensor, const uint16_t *weight,
 }
 
 /* The same for head_dim 128: 16 lanes per (row, head), 8 dims (16 bytes)
- * per lane, four heads per wave. */
-__global__ void __launch_bounds__(256)
-hk_head_rms128(uint16_t *tensor, const uint16_t *weight, uint32_t vectors,
-               float epsilon) {
-    const uint32_t vec = (blockIdx.x * blockDim.x + threadIdx.x) >> 4;
-    const uint32_t part = threadIdx.x & 15u;
-    const bool live = vec < vectors;
-    uint4 *x = (uint4 *)(tensor + (size_t)(live ? vec : 0) * 128u) + part;
+ * per lane, four heads per wave.  hk_head_rms128_vec is one lane's part of
+ * one vector, shared with the grouped form below so both round alike. */
+__device__ __forceinline__ void hk_head_rms128_vec(uint16_t *vector,
+                                                   const uint16_t *weight,
+                                                   uint32_t part, bool live,
+                                                   float epsilon) {
+    uint4 *x = (uint4 *)vector + part;
     const uint4 raw = live ? *x : make_uint4(0, 0, 0, 0);
     const uint4 wraw = ((const uint4 *)weight)[part];
     const uint32_t xw[4] = {raw.x, raw.y, raw.z, raw.w};
@@ -891,6 +890,31 @@ hk_head_rms128(uint16_t *tensor, const uint16_t *weight, uint32_t vectors,
         ow[e] = hk_pack2(v[2 * e] * inverse * hk_bf2f(ww[e] & 0xffffu),
                          v[2 * e + 1] * inverse * hk_bf2f(ww[e] >> 16));
     if (live) *x = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+}
+
+__global__ void __launch_bounds__(256)
+hk_head_rms128(uint16_t *tensor, const uint16_t *weight, uint32_t vectors,
+               float epsilon) {
+    const uint32_t vec = (blockIdx.x * blockDim.x + threadIdx.x) >> 4;
+    const bool live = vec < vectors;
+    hk_head_rms128_vec(tensor + (size_t)(live ? vec : 0) * 128u, weight,
+                       threadIdx.x & 15u, live, epsilon);
+}
+
+/* Many tensors of one shape, each with its own weight, in one launch:
+ * vector v belongs to problem v / per_problem, whose tensor and weight
+ * addresses are table[2 p] and table[2 p + 1]. */
+__global__ void __launch_bounds__(256)
+hk_head_rms128_group(const uint64_t *table, uint32_t per_problem,
+                     uint32_t vectors, float epsilon) {
+    const uint32_t vec = (blockIdx.x * blockDim.x + threadIdx.x) >> 4;
+    const bool live = vec < vectors;
+    const uint32_t v = live ? vec : 0;
+    const uint32_t p = v / per_problem;
+    uint16_t *tensor = (uint16_t *)(uintptr_t)table[2 * p];
+    const uint16_t *weight = (const uint16_t *)(uintptr_t)table[2 * p + 1];
+    hk_head_rms128_vec(tensor + (size_t)(v - p * per_problem) * 128u, weight,
+                       threadIdx.x & 15u, live, epsilon);
 }
 
 /* ------------------------------------------------- small projections */
@@ -1936,6 +1960,91 @@ int h3_gpu_head_rms_norm_bf16(h3_gpu *gpu, h3_gpu_tensor *tensor,
                            gpu->stream, HK_BF16(tensor), HK_CBF16(weight),
                            sequence, heads, head_dim, epsilon);
     return hk_op_end(gpu, "head_rms_norm", HK_KIND_DIRECT);
+}
+
+h3_gpu_tensor *h3_hip_head_norm_group_table(
+    h3_gpu *gpu, h3_gpu_tensor *const *tensors,
+    const h3_gpu_tensor *const *weights, uint32_t count, uint32_t rows,
+    uint32_t heads, uint32_t head_dim) {
+    if (!gpu) return NULL;
+    if (!count || !tensors || !weights) {
+        hk_fail(gpu, "grouped head norm table needs at least one problem");
+        return NULL;
+    }
+    if (head_dim != 128) {
+        hk_fail(gpu, "grouped head norm takes head_dim 128, not %u",
+                head_dim);
+        return NULL;
+    }
+    uint64_t *entries = (uint64_t *)calloc((size_t)count * 2, sizeof(uint64_t));
+    if (!entries) {
+        hk_fail(gpu, "out of host memory");
+        return NULL;
+    }
+    for (uint32_t p = 0; p < count; p++) {
+        if (!HK_REQ_BF16(tensors[p], (size_t)rows * heads * head_dim,
+                         "grouped head norm tensor") ||
+            !HK_REQ_BF16(weights[p], head_dim, "grouped head norm weight")) {
+            free(entries);
+            return NULL;
+        }
+        if ((((uintptr_t)tensors[p]->data | (uintptr_t)weights[p]->data) &
+             15u) != 0) {
+            free(entries);
+            hk_fail(gpu, "grouped head norm problem %u: tensors not 16-byte "
+                         "aligned", p);
+            return NULL;
+        }
+        entries[2 * p] = (uint64_t)(uintptr_t)tensors[p]->data;
+        entries[2 * p + 1] = (uint64_t)(uintptr_t)weights[p]->data;
+    }
+    h3_gpu_tensor *table = h3_gpu_tensor_from_u32(
+        gpu, (const uint32_t *)entries, (size_t)count * 4);
+    free(entries);
+    if (table) {
+        table->group_shape[0] = rows;
+        table->group_shape[1] = heads;
+        table->group_shape[2] = head_dim;
+        table->group_shape[3] = count;
+    }
+    return table;
+}
+
+int h3_hip_head_rms_norm_group_bf16(h3_gpu *gpu, const h3_gpu_tensor *table,
+                                    uint32_t first, uint32_t count,
+                                    uint32_t rows, uint32_t heads,
+                                    uint32_t head_dim, float epsilon) {
+    if (table && table->group_shape[3] == 0)
+        return hk_fail(gpu, "grouped head norm: the table was not built by "
+                            "h3_hip_head_norm_group_table");
+    if (table && (rows != table->group_shape[0] ||
+                  heads != table->group_shape[1] ||
+                  head_dim != table->group_shape[2]))
+        return hk_fail(gpu, "grouped head norm: shape %ux%ux%u differs from "
+                            "the table's %ux%ux%u", rows, heads, head_dim,
+                       table->group_shape[0], table->group_shape[1],
+                       table->group_shape[2]);
+    if (table && (uint64_t)first + count > table->group_shape[3])
+        return hk_fail(gpu, "grouped head norm: problems [%u, %u) past the "
+                            "table's %u", first, first + count,
+                       table->group_shape[3]);
+    if (!hk_require(gpu, table, ((size_t)first + count) * 4, H3_GPU_U32,
+                    "grouped head norm table") ||
+        !hk_require_active(gpu))
+        return 0;
+    const uint64_t per = (uint64_t)rows * heads;
+    const uint64_t vectors = per * count;
+    if (!vectors) return 1;
+    if (vectors > 0xffffffffull / 16u)
+        return hk_fail(gpu, "grouped head norm: %llu vectors is too many",
+                       (unsigned long long)vectors);
+    hk_op_begin(gpu, "head_rms_norm_group");
+    hipLaunchKernelGGL(hk_head_rms128_group,
+                       dim3((unsigned)((vectors + 15) / 16)), dim3(256), 0,
+                       gpu->stream,
+                       (const uint64_t *)table->data + (size_t)first * 2,
+                       (uint32_t)per, (uint32_t)vectors, epsilon);
+    return hk_op_end(gpu, "head_rms_norm_group", HK_KIND_DIRECT);
 }
 
 /* ---- projections ---- */

@@ -140,6 +140,10 @@ def lib():
         "h3_hip_sdpa_qkv_bf16": (_I, [_P, _P, _P, _U32, _U32, _U32, _F]),
         "h3_hip_linear_group_table": (_P, [_P, _P, _P, _P, _U32, _U32, _U32,
                                            _U32]),
+        "h3_hip_head_norm_group_table": (_P, [_P, _P, _P, _U32, _U32, _U32,
+                                              _U32]),
+        "h3_hip_head_rms_norm_group_bf16": (_I, [_P, _P, _U32, _U32, _U32,
+                                                 _U32, _U32, _F]),
         "h3_hip_linear_group_bf16": (_I, [_P, _P, _U32, _U32, _P, _U32, _U32,
                                           _U32]),
         "h3_gpu_layer_adaln_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _U32,

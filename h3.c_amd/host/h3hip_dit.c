@@ -33,6 +33,8 @@ struct h3hip_dit {
     /* Wan: the grouped projection's table, problems (block b's K, V) at
      * 2 b and 2 b + 1 */
     h3_gpu_tensor *ctx_table;
+    /* Wan: every block's text-key head norm, problem b = block b */
+    h3_gpu_tensor *knorm_table;
     int attention_adaln_ready;
     unsigned op_mask;
     /* H3 sampler */
@@ -232,10 +234,22 @@ h3hip_dit *h3hip_dit_create(h3_gpu *gpu, const h3hip_dit_config *config,
                 gpu, outputs, weights, biases, problems, (uint32_t)t,
                 (uint32_t)d, (uint32_t)inner);
         }
+        if (dit->ctx_table && outputs && weights &&
+            config->head_dim == 128) {
+            for (uint32_t b = 0; b < config->blocks; b++) {
+                outputs[b] = dit->blocks[b].ctx_k;
+                weights[b] = dit->blocks[b].ck_norm;
+            }
+            dit->knorm_table = h3_hip_head_norm_group_table(
+                gpu, outputs, weights, config->blocks, (uint32_t)t,
+                config->heads, config->head_dim);
+        }
         free(outputs);
         free(weights);
         free(biases);
-        if (!dit->ctx_table) ok = 0;
+        if (!dit->ctx_table ||
+            (config->head_dim == 128 && !dit->knorm_table))
+            ok = 0;
     }
     if (!ok) {
         if (error && error_size)
@@ -266,7 +280,7 @@ void h3hip_dit_free(h3hip_dit *dit) {
         dit->context, dit->mod_a, dit->mod_b, dit->qkv, dit->query,
         dit->key, dit->value, dit->attn, dit->proj, dit->cross_q,
         dit->cross_out, dit->ffn_act,
-        dit->ctx_table};
+        dit->ctx_table, dit->knorm_table};
     for (size_t i = 0; i < sizeof(shared) / sizeof(*shared); i++)
         h3_gpu_tensor_free(shared[i]);
     sampler_free(dit);
@@ -624,8 +638,8 @@ int h3hip_dit_run_blocks_ops(h3hip_dit *dit, uint32_t first, uint32_t count,
                         first + count, dit->config.blocks);
     dit->attention_adaln_ready = 0;
     if (is_wan(dit) && count && dit->config.text_rows) {
-        /* every block's cross-attention K and V of the text, in one launch,
-         * then each block's K norm */
+        /* every block's cross-attention K and V of the text in one launch,
+         * then every block's K norm in another */
         const h3hip_dit_config *c = &dit->config;
         const uint32_t t = c->text_rows, inner = c->heads * c->head_dim;
         if (!DIT_OP(K_CTX, h3_hip_linear_group_bf16(
@@ -633,13 +647,21 @@ int h3hip_dit_run_blocks_ops(h3hip_dit *dit, uint32_t first, uint32_t count,
                                dit->context, t, c->hidden, inner),
                     "cross K/V projections"))
             return 0;
-        for (uint32_t b = first; b < first + count; b++)
-            if (!DIT_OP(K_ROWS, h3_gpu_head_rms_norm_bf16(
-                                    dit->gpu, dit->blocks[b].ctx_k,
-                                    dit->blocks[b].ck_norm, t, c->heads,
-                                    c->head_dim, c->epsilon),
-                        "cross K norm"))
+        if (dit->knorm_table) {
+            if (!DIT_OP(K_ROWS, h3_hip_head_rms_norm_group_bf16(
+                                    dit->gpu, dit->knorm_table, first, count,
+                                    t, c->heads, c->head_dim, c->epsilon),
+                        "cross K norms"))
                 return 0;
+        } else {
+            for (uint32_t b = first; b < first + count; b++)
+                if (!DIT_OP(K_ROWS, h3_gpu_head_rms_norm_bf16(
+                                        dit->gpu, dit->blocks[b].ctx_k,
+                                        dit->blocks[b].ck_norm, t, c->heads,
+                                        c->head_dim, c->epsilon),
+                            "cross K norm"))
+                    return 0;
+        }
     }
     for (uint32_t b = first; b < first + count; b++) {
         const int fuse_next = b + 1 < first + count;

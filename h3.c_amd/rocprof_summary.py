@@ -138,6 +138,35 @@ def _groups(path, value="Counter_Value"):
     return out
 
 
+def _mfma_groups(path, simds=1024, xcds=8):
+    """(kernel, grid, role) -> MFMA busy % per dispatch: rocprofv3's derived
+    MfmaUtil where the run collected it, else SQ_VALU_MFMA_BUSY_CYCLES over
+    GRBM_GUI_ACTIVE (summed over the XCDs) x SIMDs, the same derivation."""
+    rows = list(csv.DictReader(open(path)))
+    if any(r["Counter_Name"] == "MfmaUtil" for r in rows):
+        return _groups(path)
+    per = defaultdict(dict)
+    meta = {}
+    for r in rows:
+        i = int(r["Dispatch_Id"])
+        per[i][r["Counter_Name"]] = float(r["Counter_Value"])
+        meta[i] = r
+    tmp = "/tmp/_mfma_util.csv"
+    with open(tmp, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(rows[0].keys()))
+        w.writeheader()
+        for i, c in per.items():
+            if "SQ_VALU_MFMA_BUSY_CYCLES" not in c or not c.get(
+                    "GRBM_GUI_ACTIVE"):
+                continue
+            r = dict(meta[i])
+            r["Counter_Name"] = "MfmaUtil"
+            r["Counter_Value"] = 100.0 * c["SQ_VALU_MFMA_BUSY_CYCLES"] / (
+                c["GRBM_GUI_ACTIVE"] / xcds * simds)
+            w.writerow(r)
+    return _groups(tmp)
+
+
 def _short(name):
     name = name.replace("void ", "")
     cut = name.find("(")
@@ -172,7 +201,7 @@ def forward_util(mfma_raw_csv, simds=1024, xcds=8):
 
 def kernels(trace_csv, mfma_csv, fetch_csv, write_csv, calib_elements):
     dur = _groups(trace_csv, "duration")
-    mfma = _groups(mfma_csv)
+    mfma = _mfma_groups(mfma_csv)
     fetch = _groups(fetch_csv)
     write = _groups(write_csv)
     cal = [k for k in fetch if "hk_elementwise8<2>" in k[0]]

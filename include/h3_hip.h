@@ -192,6 +192,24 @@ int h3_hip_linear_group_bf16(h3_gpu *gpu, const h3_gpu_tensor *table,
                              const h3_gpu_tensor *input, uint32_t rows,
                              uint32_t input_dim, uint32_t output_dim);
 
+/* A group of per-head RMS norms of one shape (rows x heads x head_dim, in
+ * place), each tensor with its own weight, as one launch: the table
+ * h3_hip_head_norm_group_table builds holds the problems' device addresses
+ * (free it with h3_gpu_tensor_free), and h3_hip_head_rms_norm_group_bf16
+ * normalises problems [first, first + count) of it, at the shape the table
+ * was built with (another shape fails with an error).  head_dim 128 and
+ * 16-byte aligned tensors only.  Each result is bit-identical to
+ * h3_gpu_head_rms_norm_bf16 on that tensor.  No reference counterpart: the
+ * Wan-shaped driver normalises every block's text keys with one launch. */
+h3_gpu_tensor *h3_hip_head_norm_group_table(
+    h3_gpu *gpu, h3_gpu_tensor *const *tensors,
+    const h3_gpu_tensor *const *weights, uint32_t count, uint32_t rows,
+    uint32_t heads, uint32_t head_dim);
+int h3_hip_head_rms_norm_group_bf16(h3_gpu *gpu, const h3_gpu_tensor *table,
+                                    uint32_t first, uint32_t count,
+                                    uint32_t rows, uint32_t heads,
+                                    uint32_t head_dim, float epsilon);
+
 /* Two projections of one input, output0 = X . weight0^T + bias0 and
  * output1 = X . weight1^T + bias1, each exactly as h3_gpu_linear_bf16
  * computes it (f32 accumulation, one bf16 rounding).  Small launches

@@ -177,6 +177,47 @@ def test_linear_group_rejects_another_shape(gpu):
         gpu.L.h3_gpu_tensor_free(plain)
 
 
+def test_head_norm_group_matches_per_tensor(gpu):
+    """h3_hip_head_rms_norm_group_bf16 normalises problems [first, first +
+    count) of a table in one launch, each bit-identical to
+    h3_gpu_head_rms_norm_bf16 on that tensor with its own weight and
+    against the oracle; problems outside the range are left alone; another
+    shape or a range past the table fails."""
+    rows, heads, hd, total, first, count = 77, 5, 128, 5, 1, 3
+    rng = np.random.default_rng(91)
+    xs = [rand_bf16(rng, rows * heads * hd) for _ in range(total)]
+    ws = [rand_bf16(rng, hd, 0.3) for _ in range(total)]
+    tg = [gpu.bf16(x) for x in xs]
+    tr = [gpu.bf16(x) for x in xs]
+    tw = [gpu.bf16(w) for w in ws]
+    P = C.c_void_p
+    table = gpu.L.h3_hip_head_norm_group_table(
+        gpu.h, (P * total)(*tg), (P * total)(*tw), total, rows, heads, hd)
+    assert table, gpu.error()
+    try:
+        gpu.run("h3_hip_head_rms_norm_group_bf16", table, first, count, rows,
+                heads, hd, 1e-6)
+        for p in range(total):
+            got = gpu.read_bf16(tg[p]).view(np.uint16)
+            if not first <= p < first + count:
+                assert np.array_equal(got, xs[p].view(np.uint16))
+                continue
+            gpu.run("h3_gpu_head_rms_norm_bf16", tr[p], tw[p], rows, heads,
+                    hd, 1e-6)
+            assert np.array_equal(got,
+                                  gpu.read_bf16(tr[p]).view(np.uint16))
+            want = oracle.head_rms_norm(xs[p], ws[p], rows, heads, hd, 1e-6)
+            assert_close(gpu.read_bf16(tg[p]), want, what=f"group norm {p}")
+        for args, what in (((0, 2, rows + 1, heads, hd), "differs"),
+                           ((0, 2, rows, heads + 1, hd), "differs"),
+                           ((4, 2, rows, heads, hd), "past the")):
+            with pytest.raises(RuntimeError, match=what):
+                gpu.run("h3_hip_head_rms_norm_group_bf16", table, *args,
+                        1e-6)
+    finally:
+        gpu.L.h3_gpu_tensor_free(table)
+
+
 def test_mfma_loop_measures_a_plausible_rate(gpu):
     """h3_hip_mfma_loop (the bench's measured MFMA ceiling): the sums are
     exact small multiples of 2^-14, so two iterations give exactly twice
