@@ -172,11 +172,14 @@ __device__ __forceinline__ void hk_tile_coords(uint32_t tile, uint32_t tiles_m,
  *   6 tile end (LDS reads done, barrier)
  *   7 the tile's index in the launch
  *   8 / 9 shader clock at 0 / 6
+ *   10 shader cycles wave 0 spent in the K loop's stage waits (its DMA
+ *      loads, then the barrier), summed over the tile's K steps
+ *   11 shader cycles wave 0 spent waiting for fragment reads in the K loop
  * h3_hip_gemm_trace_clear / _read (trace build only) reset and fetch it. */
 #ifdef HK_GEMM_TRACE
 #define HK_TRACE_WG 1024u
 #define HK_TRACE_ITERS 16u
-#define HK_TRACE_SLOTS 10u
+#define HK_TRACE_SLOTS 12u
 static __device__ uint64_t
     hk_gemm_trace[HK_TRACE_WG * HK_TRACE_ITERS * HK_TRACE_SLOTS];
 __device__ __forceinline__ void hk_trace_put(uint32_t iter, uint32_t slot,
@@ -190,10 +193,12 @@ __device__ __forceinline__ void hk_trace_put(uint32_t iter, uint32_t slot,
 #define HK_TRACE_CLOCK(p) \
     hk_trace_put(iter, (p), __builtin_amdgcn_s_memtime())
 #define HK_TRACE_VALUE(p, v) hk_trace_put(iter, (p), (v))
+#define HK_CYCLES() __builtin_amdgcn_s_memtime()
 #else
 #define HK_TRACE(p) ((void)0)
 #define HK_TRACE_CLOCK(p) ((void)0)
 #define HK_TRACE_VALUE(p, v) ((void)0)
+#define HK_CYCLES() 0ull
 #endif
 
 template <int EPI, bool GROUP = false>
@@ -411,31 +416,51 @@ hk_gemm_mfma(hk_gemm_args g) {
     read_frags(0, 0, 0);
     wait_frags(0);
 #define HK_PIN() __builtin_amdgcn_sched_barrier(0)
+#ifdef HK_GEMM_TRACE
+    uint64_t stall_stage = 0, stall_frag = 0;
+#define HK_WAIT_FRAGS(b)                                                     \
+    do {                                                                     \
+        const uint64_t c0 = HK_CYCLES();                                     \
+        wait_frags(b);                                                       \
+        stall_frag += HK_CYCLES() - c0;                                      \
+    } while (0)
+#else
+#define HK_WAIT_FRAGS(b) wait_frags(b)
+#endif
     for (uint32_t kt = 0; kt < k_steps; kt++) {
         const uint32_t stage = kt & 1u;
         /* the second half of stage kt + 1's loads (the prologue issued all
          * of stage 1's) */
         substep(0, stage, 1, kt > 0, stage ^ 1u,
                 min(kt + 1, k_steps - 1) * HK_BK * 2u, 8);
-        wait_frags(1);
+        HK_WAIT_FRAGS(1);
         substep(1, stage, 2, false, 0, 0, 0);
-        wait_frags(0);
+        HK_WAIT_FRAGS(0);
         substep(0, stage, 3, false, 0, 0, 0);
-        wait_frags(1);
+        HK_WAIT_FRAGS(1);
         /* every wave now holds the whole stage in registers; the next stage
          * is complete once every wave's loads have landed */
+#ifdef HK_GEMM_TRACE
+        const uint64_t c0 = HK_CYCLES();
+#endif
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
+#ifdef HK_GEMM_TRACE
+        stall_stage += HK_CYCLES() - c0;
+#endif
         HK_PIN();
         /* past the end the reads and loads repeat a stage no one uses
          * again, which keeps the loop free of branches around the
          * accumulators */
         substep(1, stage ^ 1u, 0, true, stage,
                 min(kt + 2, k_steps - 1) * HK_BK * 2u, 0);
-        wait_frags(0);
+        HK_WAIT_FRAGS(0);
     }
 #undef HK_PIN
+#undef HK_WAIT_FRAGS
     HK_TRACE(2);
+    HK_TRACE_VALUE(10, stall_stage);
+    HK_TRACE_VALUE(11, stall_frag);
 
     /* ---- epilogue ----
      * acc[i][j][r] = C[m][n] with

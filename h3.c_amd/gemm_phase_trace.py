@@ -38,7 +38,7 @@ SHAPES = {  # name: (M, K, N) of the Wan block at 512x512x22f
     "down": (6144, 13824, 5120),
     "up": (6144, 5120, 13824),
 }
-WG, ITERS, SLOTS = 1024, 16, 10
+WG, ITERS, SLOTS = 1024, 16, 12
 PHASES = (("prologue", 0, 1), ("main", 1, 2), ("bias", 2, 3),
           ("stage", 3, 4), ("store", 4, 5), ("drain", 5, 6))
 
@@ -103,6 +103,15 @@ def trace_shape(gpu, L, name, m, k, n, out_dir=None):
         print(f"{r:5d}  {int(sel.sum()):5d}  {start.min():7.1f}..{start.max():7.1f}"
               f"       " + "  ".join(cells) +
               f"    {tile:7.2f}  {clk:9.3f}  {end:10.1f}")
+    kst = k // 64
+    main_cyc = ((tr[:, :, 2] - tr[:, :, 1]) *
+                (tr[:, :, 9] - tr[:, :, 8]) /
+                np.maximum(tr[:, :, 6] - tr[:, :, 0], 1))[live]
+    print(f"K loop, wave 0, per 64-deep stage: "
+          f"{main_cyc.mean() / kst:.0f} shader cycles (2048 = its MFMAs "
+          f"alone), of which {tr[:, :, 10][live].mean() / kst:.0f} waiting "
+          f"at the stage's loads + barrier and "
+          f"{tr[:, :, 11][live].mean() / kst:.0f} for fragment reads")
     tot = sum(totals.values())
     print("share of tile time: " + ", ".join(
         f"{p} {100 * v / tot:.1f}%" for p, v in totals.items()))
