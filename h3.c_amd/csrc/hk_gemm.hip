@@ -201,424 +201,30 @@ __device__ __forceinline__ void hk_trace_put(uint32_t iter, uint32_t slot,
 #define HK_CYCLES() 0ull
 #endif
 
-template <int EPI, bool GROUP = false>
-__global__ void __launch_bounds__(HK_GEMM_THREADS, 1)
-__attribute__((amdgpu_waves_per_eu(1, 1)))
-hk_gemm_mfma(hk_gemm_args g) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t hk_smem[];
-    constexpr bool partial =
-        EPI == HK_EPI_PARTIAL || EPI == HK_EPI_PARTIAL_SWIGLU;
-    constexpr bool swiglu_rows =
-        EPI == HK_EPI_SWIGLU || EPI == HK_EPI_PARTIAL_SWIGLU;
-    /* the wave index is uniform: keep it (and the LDS destinations of the
-     * DMA loads derived from it) in scalar registers */
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t wm = wave & 1, wn = wave >> 1;
-
-    /* ---- workgroup -> tiles (XCD regroup, then GROUP_M bands) ----
-     * Workgroups are dealt round-robin to the 8 XCDs; the regroup gives each
-     * XCD a contiguous run of tiles in every round. */
-    const uint32_t nwg = gridDim.x;
-    uint32_t slot = blockIdx.x;
-    if ((nwg & 7u) == 0) slot = (slot & 7u) * (nwg >> 3) + (slot >> 3);
-    const uint32_t tile_count = partial ? nwg : g.tile_count;
-    uint32_t iter = 0;
-    (void)iter;
-    for (uint32_t item = slot; item < tile_count; item += nwg) {
-
-    /* Everything lane-dependent is recomputed per tile: laundering the
-     * thread index keeps the compiler from hoisting those values out of the
-     * tile loop, where they would stay live through the epilogue (which
-     * needs all 256 VGPRs) and be spilled, with scratch reloads and their
-     * vmcnt waits landing in the main loop. */
-    uint32_t tid = threadIdx.x;
-    asm volatile("" : "+v"(tid));
-    const uint32_t lane = tid & 63;
-    HK_TRACE(0);
-    HK_TRACE_CLOCK(8);
-    HK_TRACE_VALUE(7, item);
-    uint32_t pid = item;
-    uint32_t k_first = 0, split = 0, part = 0;
-    const uint16_t *wsrc = g.w;
-    /* grouped: the problem's bias and C addresses are read again by the
-     * epilogue, so that only the index stays live through the main loop */
-    uint32_t prob = 0;
-    if (GROUP) {
-        prob = pid / g.group_tiles;
-        pid -= prob * g.group_tiles;
-        wsrc = (const uint16_t *)hk_group_word(g.group, 3 * prob);
-    }
-    if (partial) {
-        split = pid / g.part_tiles;
-        part = pid - split * g.part_tiles;
-        const bool second = g.pair_tiles && part >= g.pair_tiles;
-        pid = g.tile_base + (second ? part - g.pair_tiles : part);
-        if (second) wsrc = g.w1;
-        k_first = split * g.split_steps;
-    }
-    uint32_t tile_m, tile_n;
-    hk_tile_coords(pid, g.tiles_m, g.tiles_n, tile_m, tile_n);
-    const uint32_t m0 = tile_m * HK_BM;
-
-    /* ---- staging plan ----
-     * Each operand tile is 256 rows x 8 chunks (16 B) = 2048 chunks per
-     * stage.  Direct-to-LDS buffer loads write lane i of a wave to LDS byte
-     * base + 16 i, so the swizzle is applied on the global side: wave w,
-     * load j covers LDS chunk slots p = (8 w + j) * 64 + lane, i.e. row
-     * p / 8, physical chunk p % 8, holding logical chunk (p % 8) ^ key(row).
-     * Rows past M (and W rows past the end) get an offset beyond the
-     * buffer, which the hardware returns as zeros. */
-    const __amdgpu_buffer_rsrc_t xr = hk_rsrc(g.x, g.x_bytes);
-    const __amdgpu_buffer_rsrc_t wr = hk_rsrc(wsrc, g.w_bytes);
-    uint32_t x_off[8], w_off[8];
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const uint32_t slot = (wave * 8u + j) * 64u + lane;
-        const uint32_t row = slot >> 3;
-        const uint32_t chunk = (slot & 7u) ^ hk_swz_key(row);
-        const uint32_t xm = min(m0 + row, g.m);
-        x_off[j] = xm * g.k * 2u + chunk * 16u + k_first * (HK_BK * 2u);
-        uint32_t wrow;
-        if (swiglu_rows) {
-            /* W tile rows: per wave half 64 gate rows then 64 up rows */
-            const uint32_t half = row >> 7, within = row & 127u;
-            const uint32_t col = tile_n * 128u + half * 64u + (within & 63u);
-            wrow = col < g.n ? (within >> 6) * g.n + col : 2u * g.n;
-        } else {
-            wrow = min(tile_n * HK_BN + row, g.n);
-        }
-        w_off[j] = wrow * g.k * 2u + chunk * 16u + k_first * (HK_BK * 2u);
-    }
-
-    hk_f32x16 acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
-
-    /* One 16-byte direct-to-LDS load: t in [0, 16) is the wave's t-th load
-     * of a stage, even t the X tile, odd t the W tile. */
-    auto issue_load = [&](uint32_t stage, uint32_t kb, int t) {
-        uint8_t *sx = hk_smem + stage * HK_STAGE_BYTES;
-        const int j = t >> 1;
-        const uint32_t base = (wave * 8u + j) * 1024u;
-        /* the stage's k offset goes in the scalar offset: rows past the
-         * matrix keep a lane offset beyond the buffer and still read 0 */
-        if ((t & 1) == 0)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                xr, (__attribute__((address_space(3))) void *)(sx + base), 16,
-                x_off[j], kb, 0, 0);
-        else
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                wr,
-                (__attribute__((address_space(3))) void *)(sx + HK_TILE_BYTES +
-                                                           base),
-                16, w_off[j], kb, 0, 0);
-    };
-    auto issue_loads = [&](uint32_t stage, uint32_t k0) {
-#pragma unroll
-        for (int t = 0; t < 16; t++) issue_load(stage, k0 * 2u, t);
-    };
-
-    /* ---- main loop ----
-     * Fragments are read with inline ds_read_b128 one k-step ahead of the
-     * MFMAs that consume them; the matching s_waitcnt names the fragment
-     * registers as operands, and sched_barrier(0) pins the read / MFMA /
-     * wait phases so the scheduler cannot fold them back together.  The
-     * stage barrier sits before the last 16 MFMAs of a stage: by then every
-     * wave holds all of the stage's fragments in registers, so the stage's
-     * LDS is free.  The loads of the stage after next go into it from there:
-     * the first half one per two of those 16 MFMAs, the second half one per
-     * two MFMAs of the next stage's first substep (a burst of 16 loads per
-     * wave stalls issue).  Every load still has over two substeps to land
-     * before the barrier that waits for it. */
-    const uint32_t k_steps =
-        partial ? min(g.split_steps, g.k / HK_BK - k_first)
-                              : g.k / HK_BK;
-    const uint32_t frag_row = lane & 31u;
-    const uint32_t frag_half = lane >> 5;
-    const uint32_t lds_base =
-        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)
-            hk_smem;
-    /* fragment rows are wn*128 + t*32 + frag_row (W) and wm*128 + t*32 +
-     * frag_row (X); their swizzle key only depends on frag_row & 15 */
-    const uint32_t w_row_base =
-        lds_base + HK_TILE_BYTES + (wn * 128u + frag_row) * 128u;
-    const uint32_t x_row_base = lds_base + (wm * 128u + frag_row) * 128u;
-    uint32_t chunk_off[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ks++)
-        chunk_off[ks] = ((ks * 2u + frag_half) ^ hk_swz_key(frag_row)) << 4;
-
-    hk_v4i fw[2][4], fx[2][4];
-    auto read_frags = [&](int buf, uint32_t stage, int ks) {
-        const uint32_t so = stage * HK_STAGE_BYTES + chunk_off[ks];
-        const uint32_t wa = w_row_base + so, xa = x_row_base + so;
-        asm volatile(
-            "ds_read_b128 %0, %8\n\t"
-            "ds_read_b128 %1, %8 offset:4096\n\t"
-            "ds_read_b128 %2, %8 offset:8192\n\t"
-            "ds_read_b128 %3, %8 offset:12288\n\t"
-            "ds_read_b128 %4, %9\n\t"
-            "ds_read_b128 %5, %9 offset:4096\n\t"
-            "ds_read_b128 %6, %9 offset:8192\n\t"
-            "ds_read_b128 %7, %9 offset:12288"
-            : "=&v"(fw[buf][0]), "=&v"(fw[buf][1]), "=&v"(fw[buf][2]),
-              "=&v"(fw[buf][3]), "=&v"(fx[buf][0]), "=&v"(fx[buf][1]),
-              "=&v"(fx[buf][2]), "=&v"(fx[buf][3])
-            : "v"(wa), "v"(xa));
-    };
-    auto wait_frags = [&](int buf) {
-        asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(fw[buf][0]), "+v"(fw[buf][1]), "+v"(fw[buf][2]),
-                       "+v"(fw[buf][3]), "+v"(fx[buf][0]), "+v"(fx[buf][1]),
-                       "+v"(fx[buf][2]), "+v"(fx[buf][3]));
-    };
-    /* one fragment read: idx 0-3 the W fragments, 4-7 the X fragments */
-    auto read_one = [&](int buf, uint32_t stage, int ks, int idx) {
-        const uint32_t so = stage * HK_STAGE_BYTES + chunk_off[ks];
-        if (idx < 4)
-            asm volatile("ds_read_b128 %0, %1 offset:%2"
-                         : "=&v"(fw[buf][idx])
-                         : "v"(w_row_base + so), "i"(idx * 4096));
-        else
-            asm volatile("ds_read_b128 %0, %1 offset:%2"
-                         : "=&v"(fx[buf][idx - 4])
-                         : "v"(x_row_base + so), "i"((idx - 4) * 4096));
-    };
-    /* One k-substep: 16 MFMAs on buffer `buf`, with the next substep's 8
-     * fragment reads (into the other buffer) spread one per two MFMAs and,
-     * in the last substep of a stage, the 16 loads of the stage after next
-     * one per MFMA. */
-    auto substep = [&](int buf, uint32_t rstage, int rks, bool loading,
-                       uint32_t lstage, uint32_t kb, int load_base) {
-#pragma unroll
-        for (int t = 0; t < 16; t++) {
-            const int i = t >> 2, j = t & 3;
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                __builtin_bit_cast(hk_bf16x8, fw[buf][i]),
-                __builtin_bit_cast(hk_bf16x8, fx[buf][j]), acc[i][j], 0, 0,
-                0);
-            if (t & 1) read_one(buf ^ 1, rstage, rks, t >> 1);
-            if (loading && (t & 1))
-                issue_load(lstage, kb, load_base + (t >> 1));
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
-
-    issue_loads(0, 0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    HK_TRACE(1);
-    if (k_steps > 1) issue_loads(1, HK_BK);
-    read_frags(0, 0, 0);
-    wait_frags(0);
-#define HK_PIN() __builtin_amdgcn_sched_barrier(0)
-#ifdef HK_GEMM_TRACE
-    uint64_t stall_stage = 0, stall_frag = 0;
-#define HK_WAIT_FRAGS(b)                                                     \
-    do {                                                                     \
-        const uint64_t c0 = HK_CYCLES();                                     \
-        wait_frags(b);                                                       \
-        stall_frag += HK_CYCLES() - c0;                                      \
-    } while (0)
+/* The MFMA shape of the main loop.  Full-tile launches use
+ * v_mfma_f32_16x16x32_bf16: at the same 1400 W it runs the GEMM at a
+ * higher clock than 32x32x16 (less register-file traffic per flop).  The
+ * split-K pieces keep v_mfma_f32_32x32x16_bf16: with 16x16 blocks their
+ * instances came out with accumulator copies inside the K loop.
+ * -DHK_MFMA32 builds the full-tile kernel with 32x32x16 too. */
+#ifdef HK_MFMA32
+#define HK_KERNEL_NAME hk_gemm_mfma
+#define HK_KERNEL_MFMA16 0
+#include "hk_gemm_kernel.inc"
+#undef HK_KERNEL_NAME
+#undef HK_KERNEL_MFMA16
 #else
-#define HK_WAIT_FRAGS(b) wait_frags(b)
+#define HK_KERNEL_NAME hk_gemm_mfma
+#define HK_KERNEL_MFMA16 1
+#include "hk_gemm_kernel.inc"
+#undef HK_KERNEL_NAME
+#undef HK_KERNEL_MFMA16
 #endif
-    for (uint32_t kt = 0; kt < k_steps; kt++) {
-        const uint32_t stage = kt & 1u;
-        /* the second half of stage kt + 1's loads (the prologue issued all
-         * of stage 1's) */
-        substep(0, stage, 1, kt > 0, stage ^ 1u,
-                min(kt + 1, k_steps - 1) * HK_BK * 2u, 8);
-        HK_WAIT_FRAGS(1);
-        substep(1, stage, 2, false, 0, 0, 0);
-        HK_WAIT_FRAGS(0);
-        substep(0, stage, 3, false, 0, 0, 0);
-        HK_WAIT_FRAGS(1);
-        /* every wave now holds the whole stage in registers; the next stage
-         * is complete once every wave's loads have landed */
-#ifdef HK_GEMM_TRACE
-        const uint64_t c0 = HK_CYCLES();
-#endif
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-#ifdef HK_GEMM_TRACE
-        stall_stage += HK_CYCLES() - c0;
-#endif
-        HK_PIN();
-        /* past the end the reads and loads repeat a stage no one uses
-         * again, which keeps the loop free of branches around the
-         * accumulators */
-        substep(1, stage ^ 1u, 0, true, stage,
-                min(kt + 2, k_steps - 1) * HK_BK * 2u, 0);
-        HK_WAIT_FRAGS(0);
-    }
-#undef HK_PIN
-#undef HK_WAIT_FRAGS
-    HK_TRACE(2);
-    HK_TRACE_VALUE(10, stall_stage);
-    HK_TRACE_VALUE(11, stall_frag);
-
-    /* ---- epilogue ----
-     * acc[i][j][r] = C[m][n] with
-     *   m = m0 + wm*128 + j*32 + lane%32
-     *   W-tile row = wn*128 + i*32 + (r/4)*8 + (lane/32)*4 + r%4
-     * Each lane holds 4 consecutive columns of 16 rows per (i, j), so direct
-     * stores would write 8 bytes into 32 different rows per instruction.
-     * Instead the finished bf16 tile goes through LDS (free once the last
-     * stage's loads have landed) and leaves as whole rows, 16 bytes per
-     * lane.  LDS rows are `pitch` bytes; 16-byte chunk c of row r sits at
-     * chunk c ^ (r % chunks), so both the 8-byte fragment writes (32 rows,
-     * one column group) and the row reads spread over the banks. */
-    const uint32_t sub = frag_half * 4u;
-    if (partial) {
-        /* tile-local F32, whole tile (rows and columns past the matrix are
-         * zeros that the reduction skips) */
-        float *ptile = g.partial +
-                       ((size_t)split * g.part_tiles + part) * (HK_BM * HK_BN);
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            float *prow = ptile + (wm * 128u + j * 32u + frag_row) * HK_BN;
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int q = 0; q < 4; q++)
-                    *(float4 *)(prow + wn * 128u + i * 32u + q * 8u + sub) =
-                        make_float4(acc[i][j][q * 4], acc[i][j][q * 4 + 1],
-                                    acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]);
-        }
-        return;
-    }
-    const uint16_t *bias_p =
-        GROUP ? (const uint16_t *)hk_group_word(g.group, 3 * prob + 1)
-              : g.bias;
-    uint16_t *c_p =
-        GROUP ? (uint16_t *)hk_group_word(g.group, 3 * prob + 2) : g.c;
-    constexpr uint32_t tile_cols = EPI == HK_EPI_SWIGLU ? 128u : HK_BN;
-    constexpr uint32_t pitch = tile_cols * 2u;     /* bytes per LDS row */
-    constexpr uint32_t chunks = pitch / 16u;
-    const uint32_t n0 = tile_n * tile_cols;
-    /* The bias of this lane's 16 column groups, loaded once and branch-free:
-     * columns past N read as zero through the buffer bound, and without a
-     * bias every value is -0.0, which leaves any x (signed zeros included)
-     * unchanged under x + b. */
-    hk_v2i bias2[4][4];
-    if (EPI != HK_EPI_SWIGLU) {
-        const __amdgpu_buffer_rsrc_t br =
-            hk_rsrc(bias_p, bias_p ? g.n * 2u : 0u);
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                if (bias_p) {
-                    bias2[i][q] = __builtin_amdgcn_raw_buffer_load_b64(
-                        br, (n0 + wn * 128u + i * 32u + q * 8u + sub) * 2u, 0,
-                        0);
-                } else {
-                    bias2[i][q] = hk_v2i{(int)0x80008000u, (int)0x80008000u};
-                }
-            }
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    HK_TRACE(3);
-    auto lds_put = [&](uint32_t row, uint32_t col, uint2 v) {
-        const uint32_t chunk = (col >> 3) ^ (row & (chunks - 1u));
-        *(uint2 *)(hk_smem + row * pitch + chunk * 16u + (col & 7u) * 2u) = v;
-    };
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const uint32_t row = wm * 128u + j * 32u + frag_row;
-        if (EPI == HK_EPI_SWIGLU) {
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    float out[4];
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        float gate = hk_bf2f(hk_f2bf(acc[i][j][q * 4 + e]));
-                        float up = hk_bf2f(hk_f2bf(acc[i + 2][j][q * 4 + e]));
-                        out[e] = hk_silu_f(gate) * up;
-                    }
-                    lds_put(row, wn * 64u + i * 32u + q * 8u + sub,
-                            make_uint2(hk_pack2(out[0], out[1]),
-                                       hk_pack2(out[2], out[3])));
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const uint32_t tcol = wn * 128u + i * 32u + q * 8u + sub;
-                    const hk_v2i b = bias2[i][q];
-                    float out[4];
-                    out[0] = acc[i][j][q * 4 + 0] + hk_bf2f(b[0] & 0xffffu);
-                    out[1] = acc[i][j][q * 4 + 1] + hk_bf2f((uint32_t)b[0] >> 16);
-                    out[2] = acc[i][j][q * 4 + 2] + hk_bf2f(b[1] & 0xffffu);
-                    out[3] = acc[i][j][q * 4 + 3] + hk_bf2f((uint32_t)b[1] >> 16);
-                    if (EPI == HK_EPI_GELU) {
-#pragma unroll
-                        for (int e = 0; e < 4; e++)
-                            out[e] = hk_gelu_tanh_f(hk_bf2f(hk_f2bf(out[e])));
-                    }
-                    lds_put(row, tcol,
-                            make_uint2(hk_pack2(out[0], out[1]),
-                                       hk_pack2(out[2], out[3])));
-                    /* keeps the scheduler from hoisting all 256
-                     * accumulator reads ahead of the barrier, which runs
-                     * the VGPRs out and spills */
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-        }
-    }
-    __syncthreads();
-    HK_TRACE(4);
-    /* rows leave 16 bytes per lane; N % 4 == 0, so a chunk is either whole,
-     * its first 8 bytes, or past the end.  Whole chunks are nontemporal
-     * stores: every CU writes its tile at about the same moment, and
-     * streaming the burst past the caches is 3-5% faster on the large
-     * shapes than write-allocating it. */
-    constexpr uint32_t rows_per_pass = HK_GEMM_THREADS / chunks;
-    const uint32_t chunk = tid % chunks;
-    const uint32_t col = n0 + chunk * 8u;
-    /* eight LDS reads in flight before their stores */
-    for (uint32_t row0 = tid / chunks; row0 < HK_BM;
-         row0 += 8u * rows_per_pass) {
-        uint4 v[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const uint32_t row = row0 + u * rows_per_pass;
-            v[u] = *(const uint4 *)(hk_smem + row * pitch +
-                                    ((chunk ^ (row & (chunks - 1u))) << 4));
-        }
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const uint32_t m = m0 + row0 + u * rows_per_pass;
-            if (m >= g.m || col >= g.n) continue;
-            uint16_t *dst = c_p + (size_t)m * g.n + col;
-            if (col + 8u <= g.n)
-                __builtin_nontemporal_store(
-                    hk_u32x4{v[u].x, v[u].y, v[u].z, v[u].w},
-                    (hk_u32x4 *)dst);
-            else
-                *(uint2 *)dst = make_uint2(v[u].x, v[u].y);
-        }
-    }
-    HK_TRACE(5);
-    /* the next tile's loads overwrite this tile's staged rows: every wave
-     * must be done reading them (the stores may still be in flight) */
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    HK_TRACE(6);
-    HK_TRACE_CLOCK(9);
-    iter++;
-    } /* tiles */
-}
+#define HK_KERNEL_NAME hk_gemm_mfma32
+#define HK_KERNEL_MFMA16 0
+#include "hk_gemm_kernel.inc"
+#undef HK_KERNEL_NAME
+#undef HK_KERNEL_MFMA16
 
 #ifdef HK_GEMM_TRACE
 extern "C" int h3_hip_gemm_trace_clear(void) {
@@ -951,11 +557,11 @@ static void hk_gemm_lds_setup(const struct h3_gpu *gpu) {
     (void)hipFuncSetAttribute((const void *)hk_gemm_mfma<HK_EPI_GELU>,
                               hipFuncAttributeMaxDynamicSharedMemorySize,
                               HK_GEMM_LDS);
-    (void)hipFuncSetAttribute((const void *)hk_gemm_mfma<HK_EPI_PARTIAL>,
+    (void)hipFuncSetAttribute((const void *)hk_gemm_mfma32<HK_EPI_PARTIAL>,
                               hipFuncAttributeMaxDynamicSharedMemorySize,
                               HK_GEMM_LDS);
     (void)hipFuncSetAttribute(
-        (const void *)hk_gemm_mfma<HK_EPI_PARTIAL_SWIGLU>,
+        (const void *)hk_gemm_mfma32<HK_EPI_PARTIAL_SWIGLU>,
         hipFuncAttributeMaxDynamicSharedMemorySize, HK_GEMM_LDS);
     (void)hipFuncSetAttribute((const void *)hk_gemm_mfma<HK_EPI_STORE, true>,
                               hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1053,11 +659,11 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
             g.tile_base = full;
             g.part_tiles = tail;
             if (epilogue == HK_EPI_SWIGLU)
-                hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_PARTIAL_SWIGLU>,
+                hipLaunchKernelGGL(hk_gemm_mfma32<HK_EPI_PARTIAL_SWIGLU>,
                                    dim3(tail * splits), dim3(HK_GEMM_THREADS),
                                    HK_GEMM_LDS, gpu->stream, g);
             else
-                hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_PARTIAL>,
+                hipLaunchKernelGGL(hk_gemm_mfma32<HK_EPI_PARTIAL>,
                                    dim3(tail * splits), dim3(HK_GEMM_THREADS),
                                    HK_GEMM_LDS, gpu->stream, g);
             if (epilogue == HK_EPI_SWIGLU)
@@ -1150,7 +756,7 @@ int hk_gemm_bf16_pair(struct h3_gpu *gpu, const uint16_t *x,
     g.w1 = w1; g.bias1 = b1; g.c1 = c1;
     g.group_tiles = 0;
     g.group = NULL;
-    hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_PARTIAL>, dim3(parts * splits),
+    hipLaunchKernelGGL(hk_gemm_mfma32<HK_EPI_PARTIAL>, dim3(parts * splits),
                        dim3(HK_GEMM_THREADS), HK_GEMM_LDS, gpu->stream, g);
     hipLaunchKernelGGL(hk_splitk_reduce<HK_EPI_STORE>, dim3(parts * 64),
                        dim3(256), 0, gpu->stream, g, splits);
