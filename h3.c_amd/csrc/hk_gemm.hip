@@ -8,15 +8,17 @@
  * Tiling (per 256-thread workgroup, one workgroup per CU at a time):
  *   - 256 (W rows) x 256 (X rows) output tile, K step 64;
  *   - four wave64s in a 2x2 grid, each owning a 128x128 sub-tile held as
- *     4x4 accumulators of v_mfma_f32_32x32x16_bf16 (256 f32 per lane);
+ *     8x8 accumulators of v_mfma_f32_16x16x32_bf16 (256 f32 per lane; the
+ *     split-K pieces use 4x4 of v_mfma_f32_32x32x16_bf16, see
+ *     hk_gemm_kernel.inc);
  *   - X and W tiles staged into two LDS stages by direct-to-LDS buffer
  *     loads (16 B per lane; rows past M read as zero through the buffer
  *     bound).  Once every wave holds a stage's fragments in registers, the
- *     loads of the stage after next (K step k+2) go into it, one per two
- *     MFMAs over that stage's last substep and the next stage's first, so
- *     each load has over two substeps to land;
+ *     loads of the stage after next (K step k+2) go into it, spread over
+ *     that stage's last 32-deep step, so each load has a step to a step
+ *     and a half to land;
  *   - LDS rows are 128 B (64 bf16); 16-byte chunks are XOR-swizzled with the
- *     row index so that the 32 rows a fragment read touches fall on
+ *     row index so that the 16 (or 32) rows a fragment read touches fall on
  *     distinct banks;
  *   - the MFMA computes D = W_tile . X_tile^T, so each lane's accumulator
  *     holds 4 consecutive output columns of one output row: the epilogue
