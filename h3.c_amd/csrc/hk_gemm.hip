@@ -177,6 +177,9 @@ __device__ __forceinline__ void hk_tile_coords(uint32_t tile, uint32_t tiles_m,
  *   10 shader cycles wave 0 spent in the K loop's stage waits (its DMA
  *      loads, then the barrier), summed over the tile's K steps
  *   11 shader cycles wave 0 spent waiting for fragment reads in the K loop
+ *   (10 and 11 only with -DHK_GEMM_TRACE_STALLS as well: the clock reads
+ *   inside the loop wait for their results and slow the 16x16x32 loop by
+ *   about a third, so the default trace build leaves them out)
  * h3_hip_gemm_trace_clear / _read (trace build only) reset and fetch it. */
 #ifdef HK_GEMM_TRACE
 #define HK_TRACE_WG 1024u
@@ -184,17 +187,29 @@ __device__ __forceinline__ void hk_tile_coords(uint32_t tile, uint32_t tiles_m,
 #define HK_TRACE_SLOTS 12u
 static __device__ uint64_t
     hk_gemm_trace[HK_TRACE_WG * HK_TRACE_ITERS * HK_TRACE_SLOTS];
+/* Branch-free: every lane stores, through a buffer resource, and all but
+ * thread 0 of the workgroup get an offset past the end, which the hardware
+ * drops.  A divergent branch here changed the shape of the kernel's tile
+ * loop enough for the register allocator to rotate the 16x16 accumulators
+ * through copies inside the K loop. */
 __device__ __forceinline__ void hk_trace_put(uint32_t iter, uint32_t slot,
                                              uint64_t value) {
-    if (threadIdx.x == 0 && blockIdx.x < HK_TRACE_WG && iter < HK_TRACE_ITERS)
-        hk_gemm_trace[(blockIdx.x * HK_TRACE_ITERS + iter) * HK_TRACE_SLOTS +
-                      slot] = value;
+    const __amdgpu_buffer_rsrc_t r =
+        hk_rsrc(hk_gemm_trace, (uint32_t)sizeof(hk_gemm_trace));
+    const bool mine = threadIdx.x == 0 && blockIdx.x < HK_TRACE_WG &&
+                      iter < HK_TRACE_ITERS;
+    const uint32_t off =
+        mine ? ((blockIdx.x * HK_TRACE_ITERS + iter) * HK_TRACE_SLOTS + slot) *
+                   8u
+             : 0xfffffff0u;
+    const hk_v2i v = {(int)(uint32_t)value, (int)(uint32_t)(value >> 32)};
+    __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, 0);
 }
 #define HK_TRACE(p) \
-    hk_trace_put(iter, (p), __builtin_amdgcn_s_memrealtime())
+    hk_trace_put((item - slot) / nwg, (p), __builtin_amdgcn_s_memrealtime())
 #define HK_TRACE_CLOCK(p) \
-    hk_trace_put(iter, (p), __builtin_amdgcn_s_memtime())
-#define HK_TRACE_VALUE(p, v) hk_trace_put(iter, (p), (v))
+    hk_trace_put((item - slot) / nwg, (p), __builtin_amdgcn_s_memtime())
+#define HK_TRACE_VALUE(p, v) hk_trace_put((item - slot) / nwg, (p), (v))
 #define HK_CYCLES() __builtin_amdgcn_s_memtime()
 #else
 #define HK_TRACE(p) ((void)0)

@@ -107,11 +107,13 @@ def trace_shape(gpu, L, name, m, k, n, out_dir=None):
     main_cyc = ((tr[:, :, 2] - tr[:, :, 1]) *
                 (tr[:, :, 9] - tr[:, :, 8]) /
                 np.maximum(tr[:, :, 6] - tr[:, :, 0], 1))[live]
+    stalls = tr[:, :, 10][live].any()
     print(f"K loop, wave 0, per 64-deep stage: "
           f"{main_cyc.mean() / kst:.0f} shader cycles (2048 = its MFMAs "
-          f"alone), of which {tr[:, :, 10][live].mean() / kst:.0f} waiting "
-          f"at the stage's loads + barrier and "
-          f"{tr[:, :, 11][live].mean() / kst:.0f} for fragment reads")
+          f"alone)" + (f", of which {tr[:, :, 10][live].mean() / kst:.0f} "
+                       f"waiting at the stage's loads + barrier and "
+                       f"{tr[:, :, 11][live].mean() / kst:.0f} for "
+                       f"fragment reads" if stalls else ""))
     tot = sum(totals.values())
     print("share of tile time: " + ", ".join(
         f"{p} {100 * v / tot:.1f}%" for p, v in totals.items()))
