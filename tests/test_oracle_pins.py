@@ -295,16 +295,28 @@ def _sdpa64(q, k, v, nq, nk, heads, hd, scale):
     return np.einsum("hqk,khd->qhd", p, vf).ravel()
 
 
+@pytest.mark.parametrize("seed", [0, 1, 2])
 @pytest.mark.parametrize("round_p", [False, True])
-def test_sdpa_against_float64(round_p):
+def test_sdpa_against_float64(round_p, seed):
+    """The oracle's SDPA against float64 softmax(QK^T s) V.  Rounding each
+    P to bf16 (relative error at most 2^-9) moves an output by at most
+    2^-9 sum_k p_k |v_k|; the output's own bf16 rounding adds 2^-9 |o|; f32
+    accumulation stays far below both.  The bound is twice that, so a
+    dropped scale, a transposed operand or a wrong max fails it."""
+    r = np.random.default_rng(100 + seed)
     nq, nk, heads, hd = 9, 33, 2, 128
-    q, k, v = (b(rng.standard_normal(n * heads * hd)) for n in (nq, nk, nk))
+    q, k, v = (b(r.standard_normal(n * heads * hd)) for n in (nq, nk, nk))
     scale = 1 / math.sqrt(hd)
     got = f64(oracle.sdpa(q, k, v, nq, nk, heads, hd, scale,
                           round_p=round_p))
     exact = _sdpa64(q, k, v, nq, nk, heads, hd, scale)
-    tol = 1e-3 + (1e-2 if round_p else 4e-3) * np.abs(exact)
+    spread = _sdpa64(q, k, b(np.abs(f64(v))), nq, nk, heads, hd, scale)
+    p_term = 2.0 ** -9 * spread if round_p else 0.0
+    tol = 2.0 * (p_term + 2.0 ** -9 * np.abs(exact)) + 1e-6
     assert np.all(np.abs(got - exact) <= tol)
+    # the bound has the power to see a 2% error in the scale
+    wrong = _sdpa64(q, k, v, nq, nk, heads, hd, 1.02 * scale)
+    assert np.any(np.abs(wrong - exact) > tol)
 
 
 def test_sdpa_invariants():
