@@ -739,6 +739,50 @@ def test_sdpa_head_major(gpu, n):
                                                  scale, head_major=True))
 
 
+@pytest.mark.parametrize("q_rows,kv_rows,pattern", [
+    (700, 700, "rising"),     # 11 key tiles, ragged tail
+    (1000, 1000, "rising"),   # key-range pieces: each piece's own maximum
+    (300, 513, "rising"),     # cross attention
+    (700, 700, "spikes"),     # maximum in the first tile, then jumps
+    (100, 100, "rising"),     # a single ragged key tile
+])
+def test_sdpa_running_max_moves(gpu, q_rows, kv_rows, pattern):
+    """Keys along q's direction with growing length make later key tiles
+    score far above the running maximum (by more than 32 in the exp2
+    domain), so the kernel must move its maximum and rescale O and l
+    mid-sequence, several times per row."""
+    heads, hd = 2, 128
+    rng = np.random.default_rng(kv_rows + (7 if pattern == "spikes" else 0))
+    u = rng.choice([-1.0, 1.0], hd).astype(np.float32)
+    if pattern == "rising":
+        amp = np.linspace(-2.0, 12.0, kv_rows)
+    else:
+        amp = rng.uniform(-1.0, 1.0, kv_rows)
+        amp[:8] = 4.0
+        amp[kv_rows // 3] = 9.0
+        amp[2 * kv_rows // 3] = 14.0
+    kf = (amp[:, None, None] * u[None, None, :] +
+          0.05 * rng.standard_normal((kv_rows, heads, hd)))
+    qf = 0.5 * u[None, None, :] + 0.05 * rng.standard_normal(
+        (q_rows, heads, hd))
+    q = oracle.bf16(qf.astype(np.float32).ravel())
+    k = oracle.bf16(kf.astype(np.float32).ravel())
+    v = rand_bf16(rng, kv_rows * heads * hd)
+    scale = 1.0 / math.sqrt(hd)
+    want = oracle.sdpa(q, k, v, q_rows, kv_rows, heads, hd, scale)
+    out = gpu.new_bf16(q_rows * heads * hd)
+    if q_rows == kv_rows:
+        gpu.run("h3_gpu_sdpa_bf16", out, gpu.bf16(q), gpu.bf16(k), gpu.bf16(v),
+                q_rows, heads, hd, C.c_float(scale))
+    else:
+        gpu.run("h3_gpu_sdpa_cross_bf16", out, gpu.bf16(q), gpu.bf16(k),
+                gpu.bf16(v), q_rows, kv_rows, heads, hd, C.c_float(scale))
+    assert_close(gpu.read_bf16(out), want,
+                 what=f"SDPA {q_rows}x{kv_rows} {pattern}",
+                 extra_abs=sdpa_p_rounding_bound(q, k, v, q_rows, kv_rows,
+                                                 heads, hd, scale))
+
+
 def test_sdpa_constant_keys_give_mean_value(gpu):
     """Invariant: identical keys -> uniform softmax -> output = mean of V."""
     n, heads, hd = 200, 1, 128
