@@ -48,6 +48,7 @@ def _mod_setup(rng, rows, width, slots=6, mod_rows=4):
     (260, 2048, 516, True),     # split-K, ragged M and N, 4 splits
     (600, 1088, 256, False),    # split-K with a short last split (17 steps)
     (4096, 512, 4352, True),    # 272 tiles: one full round + a split tail
+    (4100, 256, 4200, True),    # 289 tiles, full round with ragged M and N
 ])
 def test_linear_bf16(gpu, m, k, n, bias):
     rng = np.random.default_rng(m * 7 + k + n)
