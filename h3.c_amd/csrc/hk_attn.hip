@@ -62,6 +62,10 @@
 #define HK_DMA (16 / HK_WAVES) /* 1-KiB loads per wave per tile and operand */
 #define HK_STAGE_BYTES (2 * HK_TILE_BYTES)     /* K tile, then V tile */
 #define HK_ATTN_LDS (2 * HK_STAGE_BYTES)       /* 64 KiB */
+/* block-sparse launches add one flag word per key tile: up to 64 KiB more,
+ * 16384 tiles (1 Mi keys) */
+#define HK_ATTN_SPARSE_TILES 16384u
+#define HK_ATTN_SPARSE_LDS (HK_ATTN_LDS + 4u * HK_ATTN_SPARSE_TILES)
 
 
 
@@ -418,18 +422,34 @@ hk_flash_fwd(hk_attn_args a) {
         }
     }
     const bool first_block = NW_QB == 128 || wave < NW / 2;
-    /* next tile of the sparse schedule: false when done; in_a / in_b say
-     * whose list holds it */
-    auto advance = [&](uint32_t &tile, bool &in_a, bool &in_b) -> bool {
-        const uint32_t ta = ia < ea ? a.sparse_idx[ia] : 0xffffffffu;
-        const uint32_t tb = ib < eb ? a.sparse_idx[ib] : 0xffffffffu;
-        if (ta == 0xffffffffu && tb == 0xffffffffu) return false;
-        tile = min(ta, tb);
-        in_a = ta == tile;
-        in_b = tb == tile;
-        if (in_a) ia++;
-        if (in_b) ib++;
-        return true;
+    /* Block-sparse walk: the two lists become one flag word per key tile
+     * of [first_tile, dense) in LDS past the two stages (bit 0: the first
+     * block's list holds the tile, bit 1: the second's), set with LDS
+     * atomics by the whole workgroup once per work item.  Each step then
+     * finds the next tile with LDS reads; reading the lists from global
+     * memory tile by tile put a load latency before every tile's loads. */
+    uint32_t *flags = (uint32_t *)(hk_lds + HK_ATTN_LDS);
+    if (SPARSE) {
+        const uint32_t span = dense - first_tile;
+        for (uint32_t t = tid; t < span; t += NW * 64u) flags[t] = 0u;
+        __syncthreads();
+        for (uint32_t j = ia + tid; j < ea; j += NW * 64u) {
+            const uint32_t t = a.sparse_idx[j];
+            if (t >= first_tile && t < dense)
+                atomicOr(&flags[t - first_tile], 1u);
+        }
+        for (uint32_t j = ib + tid; j < eb; j += NW * 64u) {
+            const uint32_t t = a.sparse_idx[j];
+            if (t >= first_tile && t < dense)
+                atomicOr(&flags[t - first_tile], 2u);
+        }
+        __syncthreads();
+    }
+    /* the first flagged tile at or after `from`, or dense when none */
+    auto next_tile = [&](uint32_t from) -> uint32_t {
+        uint32_t t = from;
+        while (t < dense && flags[t - first_tile] == 0u) t++;
+        return t;
     };
 
     /* one tile: MFMAs and softmax on stage STAGE (compile-time, so every
@@ -476,7 +496,9 @@ hk_flash_fwd(hk_attn_args a) {
          * P, is exact up to f32 rounding. */
         const uint32_t kv0 = tile * HK_KT;
         hk_bf16x8 pf[2][2]; /* [kt][step] */
-        if constexpr (tail) {
+        /* only the last tile has keys past kv_rows; the block-sparse
+         * walk, whose steps all take this path, skips it on the others */
+        if (tail && tile + 1u == all_tiles && (a.kv_rows & (HK_KT - 1u))) {
 #pragma unroll
             for (int kt = 0; kt < 2; kt++)
 #pragma unroll
@@ -599,26 +621,24 @@ hk_flash_fwd(hk_attn_args a) {
             tile_step(S0(), first_tile + i, 0, false, true, TT());
         }
     } else {
-        uint32_t cur = 0, nxt = 0;
-        bool cur_a = false, cur_b = false, nxt_a = false, nxt_b = false;
-        bool have = advance(cur, cur_a, cur_b);
-        if (have) {
-            issue_tile(cur * HK_KT, 0);
-            }
+        /* a wave runs the MFMAs and softmax of a tile only when its own
+         * block's list holds it */
+        const uint32_t mine_bit = first_block ? 1u : 2u;
+        uint32_t cur = next_tile(first_tile);
+        if (cur < dense) issue_tile(cur * HK_KT, 0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        /* one instantiation per stage (register pressure): the key-range
-         * mask is a no-op except on the last dense tile */
-        while (have) {
-            bool more = advance(nxt, nxt_a, nxt_b);
-            tile_step(S0(), cur, nxt, more, first_block ? cur_a : cur_b,
-                      TT());
-            cur = nxt; cur_a = nxt_a; cur_b = nxt_b; have = more;
-            if (!have) break;
-            more = advance(nxt, nxt_a, nxt_b);
-            tile_step(S1(), cur, nxt, more, first_block ? cur_a : cur_b,
-                      TT());
-            cur = nxt; cur_a = nxt_a; cur_b = nxt_b; have = more;
+        /* one instantiation per stage (register pressure) */
+        while (cur < dense) {
+            uint32_t nxt = next_tile(cur + 1u);
+            tile_step(S0(), cur, nxt, nxt < dense,
+                      (flags[cur - first_tile] & mine_bit) != 0u, TT());
+            cur = nxt;
+            if (cur >= dense) break;
+            nxt = next_tile(cur + 1u);
+            tile_step(S1(), cur, nxt, nxt < dense,
+                      (flags[cur - first_tile] & mine_bit) != 0u, TT());
+            cur = nxt;
         }
     }
 
@@ -739,7 +759,8 @@ template <bool SPARSE, bool SPLIT, int NW = HK_WAVES>
 static void hk_flash_set_lds() {
     (void)hipFuncSetAttribute(
         (const void *)hk_flash_fwd<SPARSE, SPLIT, NW>,
-        hipFuncAttributeMaxDynamicSharedMemorySize, HK_ATTN_LDS);
+        hipFuncAttributeMaxDynamicSharedMemorySize,
+        SPARSE ? HK_ATTN_SPARSE_LDS : HK_ATTN_LDS);
 }
 
 template <bool SPLIT>
@@ -750,7 +771,9 @@ static void hk_flash_launch(struct h3_gpu *gpu, const hk_attn_args &a,
         hipLaunchKernelGGL((hk_flash_fwd<false, false, 4>), g, dim3(256),
                            HK_ATTN_LDS, gpu->stream, a);
     else if (masked)
-        hipLaunchKernelGGL((hk_flash_fwd<true, SPLIT>), g, b, HK_ATTN_LDS,
+        hipLaunchKernelGGL((hk_flash_fwd<true, SPLIT>), g, b,
+                           HK_ATTN_LDS + 4u * ((a.kv_rows + HK_KT - 1u) /
+                                               HK_KT),
                            gpu->stream, a);
     else
         hipLaunchKernelGGL((hk_flash_fwd<false, SPLIT>), g, b, HK_ATTN_LDS,
@@ -820,6 +843,10 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
         a.q_rows = q_rows; a.kv_rows = kv_rows; a.heads = heads;
         const bool masked = sparse && gpu->sparse_ptr &&
                             gpu->sparse_rows == q_rows && q_rows == kv_rows;
+        if (masked && (kv_rows + HK_KT - 1u) / HK_KT > HK_ATTN_SPARSE_TILES)
+            return hk_fail(gpu, "block-sparse attention takes at most %u "
+                                "key tiles of %u rows, got %u rows",
+                           HK_ATTN_SPARSE_TILES, HK_KT, kv_rows);
         /* Short cross attention (a text of at most 1024 keys) runs 4-wave,
          * 128-query workgroups, two per CU: each workgroup walks few key
          * tiles, so its Q load and O store are a large share of its time,
