@@ -422,6 +422,11 @@ hk_flash_fwd(hk_attn_args a) {
         }
     }
     const bool first_block = NW_QB == 128 || wave < NW / 2;
+    /* a wave whose 32 queries all lie past q_rows (the last query block of
+     * a ragged sequence) still stages its share of every tile and meets
+     * every barrier, but skips the MFMAs and the softmax: its output is
+     * never stored, and its split partials keep weight 0 */
+    const bool live = qbase < a.q_rows;
     /* Block-sparse walk: the two lists become one flag word per key tile
      * of [first_tile, dense) in LDS past the two stages (bit 0: the first
      * block's list holds the tile, bit 1: the second's), set with LDS
@@ -610,15 +615,15 @@ hk_flash_fwd(hk_attn_args a) {
         uint32_t i = 0;
         for (; i + 2 < n; i += 2) {
             const uint32_t t = first_tile + i;
-            tile_step(S0(), t, t + 1, true, true, NT());
-            tile_step(S1(), t + 1, t + 2, true, true, NT());
+            tile_step(S0(), t, t + 1, true, live, NT());
+            tile_step(S1(), t + 1, t + 2, true, live, NT());
         }
         if (i + 2 == n) {
-            tile_step(S0(), first_tile + i, first_tile + i + 1, true, true,
+            tile_step(S0(), first_tile + i, first_tile + i + 1, true, live,
                       NT());
-            tile_step(S1(), first_tile + i + 1, 0, false, true, TT());
+            tile_step(S1(), first_tile + i + 1, 0, false, live, TT());
         } else {
-            tile_step(S0(), first_tile + i, 0, false, true, TT());
+            tile_step(S0(), first_tile + i, 0, false, live, TT());
         }
     } else {
         /* a wave runs the MFMAs and softmax of a tile only when its own
@@ -632,12 +637,14 @@ hk_flash_fwd(hk_attn_args a) {
         while (cur < dense) {
             uint32_t nxt = next_tile(cur + 1u);
             tile_step(S0(), cur, nxt, nxt < dense,
-                      (flags[cur - first_tile] & mine_bit) != 0u, TT());
+                      live && (flags[cur - first_tile] & mine_bit) != 0u,
+                      TT());
             cur = nxt;
             if (cur >= dense) break;
             nxt = next_tile(cur + 1u);
             tile_step(S1(), cur, nxt, nxt < dense,
-                      (flags[cur - first_tile] & mine_bit) != 0u, TT());
+                      live && (flags[cur - first_tile] & mine_bit) != 0u,
+                      TT());
             cur = nxt;
         }
     }
