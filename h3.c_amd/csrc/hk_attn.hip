@@ -390,63 +390,32 @@ hk_flash_fwd(hk_attn_args a) {
         for (int r = 0; r < 16; r++) o[d][r] = 0.0f;
     float m_run = -INFINITY, l_part = 0.0f;
 
-    /* ---- key-tile schedule ----
-     * Dense: every 64-key tile in order.  Block-sparse: the workgroup's
-     * 256 queries are two 128-row query blocks of the CSR; it walks the
-     * merged (sorted) union of their tile lists, staging each tile once,
-     * and waves 0-3 (first block) / 4-7 (second block) run the MFMAs and
-     * softmax only on tiles of their own block's list.  A list's length is
-     * clamped to the dense tile count, as in the reference kernel. */
-    uint32_t ia = 0, ea = 0, ib = 0, eb = 0;
-    if (SPARSE) {
-        /* 128-row CSR blocks: one per workgroup of 128 queries, two for
-         * 256 */
-        const uint32_t qa = qblock * (NW_QB / 128u), qb = qa + 1u;
-        ia = a.sparse_ptr[qa];
-        ea = min(a.sparse_ptr[qa + 1], ia + all_tiles);
-        if (NW_QB == 256 && qb < a.sparse_blocks) {
-            ib = a.sparse_ptr[qb];
-            eb = min(a.sparse_ptr[qb + 1], ib + all_tiles);
-        }
-        if (SPLIT) {
-            /* this piece's key tiles [first_tile, dense) of the sorted
-             * lists */
-            while (ia < ea && a.sparse_idx[ia] < first_tile) ia++;
-            uint32_t e = ia;
-            while (e < ea && a.sparse_idx[e] < dense) e++;
-            ea = e;
-            while (ib < eb && a.sparse_idx[ib] < first_tile) ib++;
-            e = ib;
-            while (e < eb && a.sparse_idx[e] < dense) e++;
-            eb = e;
-        }
-    }
-    const bool first_block = NW_QB == 128 || wave < NW / 2;
     /* a wave whose 32 queries all lie past q_rows (the last query block of
      * a ragged sequence) still stages its share of every tile and meets
      * every barrier, but skips the MFMAs and the softmax: its output is
      * never stored, and its split partials keep weight 0 */
     const bool live = qbase < a.q_rows;
-    /* Block-sparse walk: the two lists become one flag word per key tile
-     * of [first_tile, dense) in LDS past the two stages (bit 0: the first
-     * block's list holds the tile, bit 1: the second's), set with LDS
-     * atomics by the whole workgroup once per work item.  Each step then
-     * finds the next tile with LDS reads; reading the lists from global
-     * memory tile by tile put a load latency before every tile's loads. */
+
+    /* ---- key-tile schedule ----
+     * Dense: every 64-key tile in order.  Block-sparse (128-query
+     * workgroups, one 128-row block of the CSR each): the kept tiles of
+     * [first_tile, dense) in order.  The list's length is clamped to the
+     * dense tile count, as in the reference kernel.  It becomes one flag
+     * word per key tile in LDS past the two stages, set by the whole
+     * workgroup once per work item, and each step finds the next tile with
+     * LDS reads: reading the list from global memory at every step put a
+     * load's latency before each tile's loads. */
+    static_assert(!SPARSE || NW == 4, "block-sparse walks one 128-row block");
     uint32_t *flags = (uint32_t *)(hk_lds + HK_ATTN_LDS);
     if (SPARSE) {
+        const uint32_t first = a.sparse_ptr[qblock];
+        const uint32_t end = min(a.sparse_ptr[qblock + 1], first + all_tiles);
         const uint32_t span = dense - first_tile;
         for (uint32_t t = tid; t < span; t += NW * 64u) flags[t] = 0u;
         __syncthreads();
-        for (uint32_t j = ia + tid; j < ea; j += NW * 64u) {
+        for (uint32_t j = first + tid; j < end; j += NW * 64u) {
             const uint32_t t = a.sparse_idx[j];
-            if (t >= first_tile && t < dense)
-                atomicOr(&flags[t - first_tile], 1u);
-        }
-        for (uint32_t j = ib + tid; j < eb; j += NW * 64u) {
-            const uint32_t t = a.sparse_idx[j];
-            if (t >= first_tile && t < dense)
-                atomicOr(&flags[t - first_tile], 2u);
+            if (t >= first_tile && t < dense) flags[t - first_tile] = 1u;
         }
         __syncthreads();
     }
@@ -626,9 +595,6 @@ hk_flash_fwd(hk_attn_args a) {
             tile_step(S0(), first_tile + i, 0, false, live, TT());
         }
     } else {
-        /* a wave runs the MFMAs and softmax of a tile only when its own
-         * block's list holds it */
-        const uint32_t mine_bit = first_block ? 1u : 2u;
         uint32_t cur = next_tile(first_tile);
         if (cur < dense) issue_tile(cur * HK_KT, 0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -636,15 +602,11 @@ hk_flash_fwd(hk_attn_args a) {
         /* one instantiation per stage (register pressure) */
         while (cur < dense) {
             uint32_t nxt = next_tile(cur + 1u);
-            tile_step(S0(), cur, nxt, nxt < dense,
-                      live && (flags[cur - first_tile] & mine_bit) != 0u,
-                      TT());
+            tile_step(S0(), cur, nxt, nxt < dense, live, TT());
             cur = nxt;
             if (cur >= dense) break;
             nxt = next_tile(cur + 1u);
-            tile_step(S1(), cur, nxt, nxt < dense,
-                      live && (flags[cur - first_tile] & mine_bit) != 0u,
-                      TT());
+            tile_step(S1(), cur, nxt, nxt < dense, live, TT());
             cur = nxt;
         }
     }
@@ -722,29 +684,30 @@ hk_flash_fwd(hk_attn_args a) {
 /* Combines the key-range pieces of the split work items: per query, with
  * the pieces' running maxima m_p (exp2 domain), sums l_p and unnormalised
  * O_p, O = sum_p 2^(m_p - M) O_p / sum_p 2^(m_p - M) l_p, M = max_p m_p.
- * 8 queries per workgroup, 4 dims per thread. */
+ * 8 queries per workgroup, 4 dims per thread; QB queries per work item. */
+template <uint32_t QB>
 __global__ void __launch_bounds__(256) hk_flash_combine(hk_attn_args a) {
-    const uint32_t titem = blockIdx.x / (HK_QB / 8u);
-    const uint32_t ql = (blockIdx.x % (HK_QB / 8u)) * 8u + (threadIdx.x >> 5);
+    const uint32_t titem = blockIdx.x / (QB / 8u);
+    const uint32_t ql = (blockIdx.x % (QB / 8u)) * 8u + (threadIdx.x >> 5);
     const uint32_t d4 = (threadIdx.x & 31u) * 4u;
     const uint32_t item = a.full_units + titem;
     const uint32_t qblock = item % a.q_blocks, head = item / a.q_blocks;
-    const uint32_t q = qblock * HK_QB + ql;
+    const uint32_t q = qblock * QB + ql;
     if (q >= a.q_rows) return;
     const size_t first = (size_t)titem * a.pieces;
     float top = -INFINITY;
     for (uint32_t p = 0; p < a.pieces; p++)
-        top = fmaxf(top, a.part_ml[((first + p) * HK_QB + ql) * 2u]);
+        top = fmaxf(top, a.part_ml[((first + p) * QB + ql) * 2u]);
     float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     float l = 0.0f;
     for (uint32_t p = 0; p < a.pieces; p++) {
         const float2 ml =
-            *(const float2 *)(a.part_ml + ((first + p) * HK_QB + ql) * 2u);
+            *(const float2 *)(a.part_ml + ((first + p) * QB + ql) * 2u);
         /* a sparse piece may hold no key tile of this query block */
         const float w =
             ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - top);
         const float4 op = *(const float4 *)(a.part_o +
-                                            ((first + p) * HK_QB + ql) * HK_HD +
+                                            ((first + p) * QB + ql) * HK_HD +
                                             d4);
         sum.x += w * op.x; sum.y += w * op.y;
         sum.z += w * op.z; sum.w += w * op.w;
@@ -772,16 +735,16 @@ static void hk_flash_set_lds() {
 
 template <bool SPLIT>
 static void hk_flash_launch(struct h3_gpu *gpu, const hk_attn_args &a,
-                            bool masked, uint32_t grid, bool narrow) {
+                            bool masked, uint32_t grid, bool four) {
     const dim3 g(grid), b(HK_THREADS);
-    if (narrow)
+    const uint32_t sparse_lds =
+        HK_ATTN_LDS + 4u * ((a.kv_rows + HK_KT - 1u) / HK_KT);
+    if (four && masked)
+        hipLaunchKernelGGL((hk_flash_fwd<true, SPLIT, 4>), g, dim3(256),
+                           sparse_lds, gpu->stream, a);
+    else if (four)
         hipLaunchKernelGGL((hk_flash_fwd<false, false, 4>), g, dim3(256),
                            HK_ATTN_LDS, gpu->stream, a);
-    else if (masked)
-        hipLaunchKernelGGL((hk_flash_fwd<true, SPLIT>), g, b,
-                           HK_ATTN_LDS + 4u * ((a.kv_rows + HK_KT - 1u) /
-                                               HK_KT),
-                           gpu->stream, a);
     else
         hipLaunchKernelGGL((hk_flash_fwd<false, SPLIT>), g, b, HK_ATTN_LDS,
                            gpu->stream, a);
@@ -839,10 +802,10 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
         const uint64_t lds_bit = 1ull << (gpu->device & 63);
         if (!(hk_attn_lds_ready & lds_bit)) {
             hk_flash_set_lds<false, false>();
-            hk_flash_set_lds<true, false>();
             hk_flash_set_lds<false, true>();
-            hk_flash_set_lds<true, true>();
             hk_flash_set_lds<false, false, 4>();
+            hk_flash_set_lds<true, false, 4>();
+            hk_flash_set_lds<true, true, 4>();
             hk_attn_lds_ready |= lds_bit;
         }
         hk_attn_args a;
@@ -859,7 +822,13 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
          * tiles, so its Q load and O store are a large share of its time,
          * and the second workgroup's tiles overlap them. */
         const bool narrow = !masked && q_rows != kv_rows && kv_rows <= 1024;
-        const uint32_t qb_rows = narrow ? 128u : HK_QB;
+        /* Block-sparse attention runs the same 128-query workgroups: each
+         * then walks its own query block's tile list.  A 256-query
+         * workgroup would walk the union of two blocks' lists, and where they
+         * differ (the window mask keeps 38 and 27 of 38 tiles in adjacent
+         * blocks) half of its waves idle on the other block's tiles. */
+        const bool four = narrow || masked;
+        const uint32_t qb_rows = four ? 128u : HK_QB;
         a.q_blocks = (q_rows + qb_rows - 1) / qb_rows;
         a.q_bytes = (uint32_t)q_bytes;
         a.kv_bytes = (uint32_t)kv_bytes;
@@ -886,7 +855,8 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
          * CUs, when that takes at most 0.6 of a round instead of one; a
          * combine kernel merges the pieces' partial softmax. */
         const uint32_t cus = (gpu->num_cus > 0 ? (uint32_t)gpu->num_cus
-                                               : 256u) * HK_WG_PER_CU;
+                                               : 256u) *
+                             (four ? 2u : (uint32_t)HK_WG_PER_CU);
         const uint32_t kv_tiles = (kv_rows + HK_KT - 1) / HK_KT;
         const uint32_t tail = units % cus;
         uint32_t pieces = 1;
@@ -910,7 +880,7 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
             pieces = (kv_tiles + per - 1) / per;
             parts = (size_t)tail * pieces;
         }
-        const size_t part_bytes = parts * HK_QB * (HK_HD + 2) * sizeof(float);
+        const size_t part_bytes = parts * qb_rows * (HK_HD + 2) * sizeof(float);
         if (table_bytes + keys_bytes + part_bytes) {
             uint8_t *buf = (uint8_t *)hk_splitk_space(
                 gpu, table_bytes + keys_bytes + part_bytes);
@@ -932,18 +902,23 @@ int hk_attention_bf16(struct h3_gpu *gpu, const uint16_t *q,
             if (parts) {
                 float *pf = (float *)(buf + table_bytes + keys_bytes);
                 a.part_o = pf;
-                a.part_ml = pf + parts * HK_QB * HK_HD;
+                a.part_ml = pf + parts * qb_rows * HK_HD;
                 a.full_units = units - tail;
                 a.pieces = pieces;
             }
         }
         if (a.full_units)
-            hk_flash_launch<false>(gpu, a, masked, a.full_units, narrow);
+            hk_flash_launch<false>(gpu, a, masked, a.full_units, four);
         if (pieces > 1) {
-            hk_flash_launch<true>(gpu, a, masked, tail * pieces, false);
-            hipLaunchKernelGGL(hk_flash_combine, dim3(tail * (HK_QB / 8)),
-                               dim3(256),
-                               0, gpu->stream, a);
+            hk_flash_launch<true>(gpu, a, masked, tail * pieces, four);
+            if (four)
+                hipLaunchKernelGGL(hk_flash_combine<128>,
+                                   dim3(tail * (128 / 8)), dim3(256), 0,
+                                   gpu->stream, a);
+            else
+                hipLaunchKernelGGL(hk_flash_combine<HK_QB>,
+                                   dim3(tail * (HK_QB / 8)), dim3(256), 0,
+                                   gpu->stream, a);
         }
         return 1;
     }
