@@ -21,7 +21,8 @@
  *   - K and V are staged row-major by direct-to-LDS loads, with XOR
  *     swizzles on 16-byte chunks (hk_k_swz, hk_v_swz);
  *   - 8 wave64s x 32 queries = 256 queries per workgroup (4 wave64s and
- *     two workgroups per CU for cross attention over at most 1024 keys),
+ *     two workgroups per CU for cross attention over at most 1024 keys
+ *     and for block-sparse attention, one CSR query block each),
  *     64-key tiles,
  *     double-buffered LDS (2 x 32 KiB) with the next tile's global loads in
  *     flight during the current tile's 32 MFMAs per wave.  At 32 queries a
@@ -59,7 +60,6 @@
 #define HK_THREADS (HK_WAVES * 64)
 #define HK_QB (HK_WAVES * 32) /* queries per workgroup */
 #define HK_WG_PER_CU (8 / HK_WAVES) /* workgroups per CU: two waves per SIMD */
-#define HK_DMA (16 / HK_WAVES) /* 1-KiB loads per wave per tile and operand */
 #define HK_STAGE_BYTES (2 * HK_TILE_BYTES)     /* K tile, then V tile */
 #define HK_ATTN_LDS (2 * HK_STAGE_BYTES)       /* 64 KiB */
 /* block-sparse launches add one flag word per key tile: up to 64 KiB more,
