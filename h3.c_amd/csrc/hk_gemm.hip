@@ -17,6 +17,11 @@
  *     loads of the stage after next (K step k+2) go into it, spread over
  *     that stage's last 32-deep step, so each load has a step to a step
  *     and a half to land;
+ *   - that is too short for lines that come from HBM, and in the forward
+ *     both operands do (weights are read once per forward, activations
+ *     were stored nontemporally), so the K loop also prefetches into L2
+ *     the lines HK_GEMM_PF stages further on (4-byte loads, the lines
+ *     split among the tiles that share them);
  *   - LDS rows are 128 B (64 bf16); 16-byte chunks are XOR-swizzled with the
  *     row index so that the 16 (or 32) rows a fragment read touches fall on
  *     distinct banks;
@@ -53,7 +58,11 @@
 #define HK_GEMM_THREADS 256
 #define HK_TILE_BYTES (HK_BM * HK_BK * 2)       /* 32 KiB per operand */
 #define HK_STAGE_BYTES (2 * HK_TILE_BYTES)      /* X tile then W tile */
-#define HK_GEMM_LDS (HK_STAGES * HK_STAGE_BYTES) /* 128 KiB */
+/* L2 prefetch distance of the 16x16x32 kernel's K loop, in 64-deep
+ * stages past the stage loads' k step */
+#define HK_GEMM_PF 2
+/* + 256 bytes that the L2 prefetch loads write and nothing reads */
+#define HK_GEMM_LDS (HK_STAGES * HK_STAGE_BYTES + 256) /* 128 KiB + 256 */
 #define HK_GROUP_M 8
 
 typedef int hk_v4i __attribute__((ext_vector_type(4)));

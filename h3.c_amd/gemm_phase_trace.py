@@ -32,11 +32,14 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, HERE)
 import h3hip  # noqa: E402
 
-SHAPES = {  # name: (M, K, N) of the Wan block at 512x512x22f
+SHAPES = {  # name: (M, K, N); the Wan block at 512x512x22f
     "qkv": (6144, 5120, 15360),
     "out": (6144, 5120, 5120),
     "down": (6144, 13824, 5120),
     "up": (6144, 5120, 13824),
+    # the H3 block at its real shape (2378 rows, hidden 5376, SwiGLU 14336)
+    "h3out": (2378, 5376, 5376),
+    "h3fc2": (2378, 14336, 5376),
 }
 WG, ITERS, SLOTS = 1024, 16, 12
 PHASES = (("prologue", 0, 1), ("main", 1, 2), ("bias", 2, 3),

@@ -1,12 +1,16 @@
-"""The MFMA GEMM's K loop, as compiled, moves no accumulator and touches no
-scratch memory.
+"""The MFMA GEMM's K loop, as compiled, moves no accumulator, touches no
+scratch memory, and waits for its loads with vmcnt(2) only.
 
 The 16x16x32 kernel holds 64 accumulator blocks in all 256 AGPRs.  Small
 changes around the loop (an extra live value, a divergent branch in the
 tile loop) have made the register allocator rotate those blocks through
 `v_accvgpr_mov` / `v_accvgpr_write` copies inside the K loop, or spill into
 scratch there, which cost the split-K instances 60-150% of their time with
-correct results.  This test compiles csrc/hk_gemm.hip as the Makefile does
+correct results.  The 16x16x32 instances keep two L2 prefetch loads in
+flight across the stage wait; a vmcnt(0) there (which the compiler adds
+for a barrier with a fence) quietly cancels the prefetch, and the cold-
+weight launches of the forward lose 4-10%.  This test compiles
+csrc/hk_gemm.hip as the Makefile does
 (and as the phase-trace build does), takes the instructions between the
 first and the last MFMA of every kernel instance, and requires none of
 those.  It needs hipcc, not a GPU.
@@ -56,8 +60,17 @@ def _k_loop_offenders(extra):
         body = text[start:end]
         mfma = [i for i, l in enumerate(body) if "v_mfma_" in l]
         assert len(mfma) == 128, (name, len(mfma))
-        found[name] = [l.strip() for l in body[mfma[0]:mfma[-1]]
-                       if BAD.search(l)]
+        loop = body[mfma[0]:mfma[-1]]
+        found[name] = [l.strip() for l in loop if BAD.search(l)]
+        if "mfma32" not in sym:
+            waits = [int(m.group(1)) for l in loop
+                     for m in [re.search(r"s_waitcnt\b.*vmcnt\((\d+)\)", l)]
+                     if m]
+            pf = [l for l in loop if re.search(r"buffer_load_dword\b.*\blds\b", l)]
+            if waits != [2]:
+                found[name].append(f"stage waits vmcnt{waits}, want [2]")
+            if len(pf) != 2:
+                found[name].append(f"{len(pf)} prefetch loads, want 2")
     return found
 
 
