@@ -29,6 +29,53 @@ def _mod_setup(rng, rows, width, slots=6, mod_rows=4):
 
 # ------------------------------------------------------------------ GEMM
 
+@pytest.mark.parametrize("m,k,n,bias,mlp", [
+    (4096, 1024, 8192, True, False),   # 512 tiles: two full rounds
+    (2378, 1024, 5376, False, False),  # H3 rows: 210 tiles, bands of 8 + 2
+    (2378, 512, 4608, False, True),    # MLP: fc1 with the SwiGLU epilogue
+])
+def test_linear_repeats_bit_exactly(gpu, m, k, n, bias, mlp):
+    """The K loop keeps its two L2 prefetch loads in flight across the
+    stage wait (vmcnt(2)), relying on loads retiring in issue order.  A
+    stage read before its loads landed would show as results that change
+    from run to run: the first run matches the oracle, and four more, each
+    after an unrelated GEMM over other buffers, match it bit for bit.  For
+    the MLP, n is the FFN width (fc1 has 2 n rows, fc2 brings it back to
+    k)."""
+    rng = np.random.default_rng(m + k + n)
+    x = rand_bf16(rng, m * k)
+    w = rand_bf16(rng, (2 * n if mlp else n) * k, 0.05)
+    w2 = rand_bf16(rng, k * n, 0.05) if mlp else None
+    b = rand_bf16(rng, n, 0.1) if bias else None
+    tx, tw = gpu.bf16(x), gpu.bf16(w)
+    tw2 = gpu.bf16(w2) if mlp else None
+    tb = gpu.bf16(b) if bias else None
+    to = gpu.new_bf16(m * (k if mlp else n))
+    om, ok_, on = 2048, 2048, 8192
+    ox = gpu.bf16(rand_bf16(rng, om * ok_))
+    ow = gpu.bf16(rand_bf16(rng, on * ok_, 0.05))
+    oo = gpu.new_bf16(om * on)
+
+    def run():
+        if mlp:
+            gpu.run("h3_gpu_mlp_bf16", to, tx, tw, tw2, m, k, n, k)
+        else:
+            gpu.run("h3_gpu_linear_bf16", to, tx, tw, tb, m, k, n)
+        return gpu.read_bf16(to)
+
+    first = run()
+    if mlp:
+        want = oracle.mlp(x, w, w2, m, k, n)
+        assert_close(first, want, what=f"MLP {m}x{k}x{n}", chained=1)
+    else:
+        want = oracle.linear(x, w, b, m, k, n)
+        assert_close(first, want, what=f"linear {m}x{k}x{n}")
+    for rep in range(4):
+        gpu.run("h3_gpu_linear_bf16", oo, ox, ow, None, om, ok_, on)
+        again = run()
+        assert np.array_equal(again, first), f"repeat {rep + 1} differs"
+
+
 @pytest.mark.parametrize("m,k,n,bias", [
     (32, 256, 256, False),      # reference test_cuda_core.c linear shape
     (100, 512, 768, True),      # ragged M
