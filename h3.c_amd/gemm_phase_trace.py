@@ -19,7 +19,7 @@ The launch's own duration, from HIP events around an untraced launch of the
 product library in a separate process, is printed by bench.py; here the
 traced launch is timed the same way for reference.
 
-    python3 h3.c_amd/gemm_phase_trace.py [--shapes qkv,out,down]
+    python3 h3.c_amd/gemm_phase_trace.py [--shapes qkv,out,down] [--cold]
 """
 import argparse
 import ctypes as C
@@ -46,20 +46,32 @@ PHASES = (("prologue", 0, 1), ("main", 1, 2), ("bias", 2, 3),
           ("stage", 3, 4), ("store", 4, 5), ("drain", 5, 6))
 
 
-def trace_shape(gpu, L, name, m, k, n, out_dir=None):
-    x, w, o = gpu.new_bf16(m * k), gpu.new_bf16(n * k), gpu.new_bf16(m * n)
-    b = gpu.new_bf16(n)
+def trace_shape(gpu, L, name, m, k, n, out_dir=None, cold=False):
+    # cold: X and W in enough copies to pass 700 MB, more than the 256 MB
+    # Infinity Cache holds, and the traced launch reads the copy used
+    # longest ago, as the forward reads every block's own weights
+    copies = max(2, int(700e6 // ((m * k + n * k) * 2)) + 1) if cold else 1
+    xs = [gpu.new_bf16(m * k) for _ in range(copies)]
+    ws = [gpu.new_bf16(n * k) for _ in range(copies)]
+    o, b = gpu.new_bf16(m * n), gpu.new_bf16(n)
     gpu.begin()
-    L.h3_gpu_fill_normal_bf16(gpu.h, x, 0, m * k, 1, 0.0, 1.0)
-    L.h3_gpu_fill_normal_bf16(gpu.h, w, 0, n * k, 2, 0.0, 0.02)
+    for i in range(copies):
+        L.h3_gpu_fill_normal_bf16(gpu.h, xs[i], 0, m * k, 1 + 10 * i, 0.0,
+                                  1.0)
+        L.h3_gpu_fill_normal_bf16(gpu.h, ws[i], 0, n * k, 2 + 10 * i, 0.0,
+                                  0.02)
     L.h3_gpu_fill_normal_bf16(gpu.h, b, 0, n, 3, 0.0, 0.02)
     gpu.submit()
+    sel = [0]
 
     def launch():
-        gpu.check(L.h3_gpu_linear_bf16(gpu.h, o, x, w, b, m, k, n), name)
+        i = sel[0] % copies
+        sel[0] += 1
+        gpu.check(L.h3_gpu_linear_bf16(gpu.h, o, xs[i], ws[i], b, m, k, n),
+                  name)
 
     gpu.begin()
-    for _ in range(3):
+    for _ in range(3 * copies):
         launch()
     gpu.submit()
     if not L.h3_hip_gemm_trace_clear():
@@ -74,13 +86,14 @@ def trace_shape(gpu, L, name, m, k, n, out_dir=None):
     tr = np.zeros(WG * ITERS * SLOTS, np.uint64)
     if not L.h3_hip_gemm_trace_read(tr.ctypes.data_as(C.c_void_p), tr.size):
         raise RuntimeError("trace read failed")
-    for t in (x, w, o, b):
+    for t in xs + ws + [o, b]:
         gpu.free(t)
     tr = tr.reshape(WG, ITERS, SLOTS).astype(np.int64)
     live = tr[:, :, 6] != 0
     t0 = tr[:, :, 0][live].min()
     tiles = ((m + 255) // 256) * ((n + 255) // 256)
-    print(f"\n{name}: M={m} K={k} N={n}, {tiles} tiles, "
+    print(f"\n{name}{' (cold operands, %d copies)' % copies if cold else ''}: "
+          f"M={m} K={k} N={n}, {tiles} tiles, "
           f"{int(live[:, 0].sum())} workgroups; traced launch "
           f"{ms.value * 1e3:.1f} us (event), first tile start to last tile "
           f"end {(tr[:, :, 6][live].max() - t0) / 100.0:.1f} us")
@@ -142,6 +155,9 @@ def trace_shape(gpu, L, name, m, k, n, out_dir=None):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--shapes", default="qkv,out,down")
+    ap.add_argument("--cold", action="store_true",
+                    help="rotate X and W over copies larger than the "
+                         "Infinity Cache (the forward's case)")
     ap.add_argument("--save", default=None,
                     help="directory for the raw traces (.npy)")
     args = ap.parse_args()
@@ -150,7 +166,8 @@ def main():
     gpu = h3hip.Gpu()
     try:
         for name in args.shapes.split(","):
-            trace_shape(gpu, L, name, *SHAPES[name], out_dir=args.save)
+            trace_shape(gpu, L, name, *SHAPES[name], out_dir=args.save,
+                        cold=args.cold)
     finally:
         gpu.close()
 
