@@ -65,7 +65,7 @@ OPS_GEMM, OPS_ACT, OPS_ATTN, OPS_ROWS, OPS_CTX = 1, 2, 4, 8, 16
 KERNEL_NAMES = {
     "gemm_plain": "hk_gemm_mfma<0, false> (QKV, out, cross q, cross out, FFN "
                   "down)",
-    "gemm_gelu": "hk_gemm_mfma<2, false> + split tail hk_gemm_mfma32<3> "
+    "gemm_gelu": "hk_gemm_mfma<2, false> + split tail hk_gemm_mfma<3> "
                  "(FFN up + GELU)",
     "context_kv": "grouped hk_gemm_mfma<0, true>: the text's cross K/V of "
                   "all blocks in one launch",

@@ -9,8 +9,7 @@
  *   - 256 (W rows) x 256 (X rows) output tile, K step 64;
  *   - four wave64s in a 2x2 grid, each owning a 128x128 sub-tile held as
  *     8x8 accumulators of v_mfma_f32_16x16x32_bf16 (256 f32 per lane; the
- *     split-K pieces use 4x4 of v_mfma_f32_32x32x16_bf16, see
- *     hk_gemm_kernel.inc);
+ *     kernel body is in hk_gemm_kernel.inc);
  *   - X and W tiles staged into two LDS stages by direct-to-LDS buffer
  *     loads (16 B per lane; rows past M read as zero through the buffer
  *     bound).  Once every wave holds a stage's fragments in registers, the
@@ -227,27 +226,17 @@ __device__ __forceinline__ void hk_trace_put(uint32_t iter, uint32_t slot,
 #define HK_CYCLES() 0ull
 #endif
 
-/* The MFMA shape of the main loop.  Full-tile launches use
- * v_mfma_f32_16x16x32_bf16: at the same 1400 W it runs the GEMM at a
- * higher clock than 32x32x16 (less register-file traffic per flop).  The
- * split-K pieces keep v_mfma_f32_32x32x16_bf16: with 16x16 blocks their
- * instances came out with accumulator copies inside the K loop.
- * -DHK_MFMA32 builds the full-tile kernel with 32x32x16 too. */
+/* The MFMA shape of the main loop: v_mfma_f32_16x16x32_bf16 for every
+ * launch, full tiles and split-K pieces.  At the same 1400 W it runs the
+ * GEMM at a higher clock than 32x32x16 (less register-file traffic per
+ * flop).  -DHK_MFMA32 builds the kernel with 32x32x16 (4x4 blocks) instead,
+ * for comparison. */
+#define HK_KERNEL_NAME hk_gemm_mfma
 #ifdef HK_MFMA32
-#define HK_KERNEL_NAME hk_gemm_mfma
 #define HK_KERNEL_MFMA16 0
-#include "hk_gemm_kernel.inc"
-#undef HK_KERNEL_NAME
-#undef HK_KERNEL_MFMA16
 #else
-#define HK_KERNEL_NAME hk_gemm_mfma
 #define HK_KERNEL_MFMA16 1
-#include "hk_gemm_kernel.inc"
-#undef HK_KERNEL_NAME
-#undef HK_KERNEL_MFMA16
 #endif
-#define HK_KERNEL_NAME hk_gemm_mfma32
-#define HK_KERNEL_MFMA16 0
 #include "hk_gemm_kernel.inc"
 #undef HK_KERNEL_NAME
 #undef HK_KERNEL_MFMA16
@@ -583,11 +572,11 @@ static void hk_gemm_lds_setup(const struct h3_gpu *gpu) {
     (void)hipFuncSetAttribute((const void *)hk_gemm_mfma<HK_EPI_GELU>,
                               hipFuncAttributeMaxDynamicSharedMemorySize,
                               HK_GEMM_LDS);
-    (void)hipFuncSetAttribute((const void *)hk_gemm_mfma32<HK_EPI_PARTIAL>,
+    (void)hipFuncSetAttribute((const void *)hk_gemm_mfma<HK_EPI_PARTIAL>,
                               hipFuncAttributeMaxDynamicSharedMemorySize,
                               HK_GEMM_LDS);
     (void)hipFuncSetAttribute(
-        (const void *)hk_gemm_mfma32<HK_EPI_PARTIAL_SWIGLU>,
+        (const void *)hk_gemm_mfma<HK_EPI_PARTIAL_SWIGLU>,
         hipFuncAttributeMaxDynamicSharedMemorySize, HK_GEMM_LDS);
     (void)hipFuncSetAttribute((const void *)hk_gemm_mfma<HK_EPI_STORE, true>,
                               hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -685,11 +674,11 @@ int hk_gemm_bf16(struct h3_gpu *gpu, const uint16_t *x, const uint16_t *w,
             g.tile_base = full;
             g.part_tiles = tail;
             if (epilogue == HK_EPI_SWIGLU)
-                hipLaunchKernelGGL(hk_gemm_mfma32<HK_EPI_PARTIAL_SWIGLU>,
+                hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_PARTIAL_SWIGLU>,
                                    dim3(tail * splits), dim3(HK_GEMM_THREADS),
                                    HK_GEMM_LDS, gpu->stream, g);
             else
-                hipLaunchKernelGGL(hk_gemm_mfma32<HK_EPI_PARTIAL>,
+                hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_PARTIAL>,
                                    dim3(tail * splits), dim3(HK_GEMM_THREADS),
                                    HK_GEMM_LDS, gpu->stream, g);
             if (epilogue == HK_EPI_SWIGLU)
@@ -782,7 +771,7 @@ int hk_gemm_bf16_pair(struct h3_gpu *gpu, const uint16_t *x,
     g.w1 = w1; g.bias1 = b1; g.c1 = c1;
     g.group_tiles = 0;
     g.group = NULL;
-    hipLaunchKernelGGL(hk_gemm_mfma32<HK_EPI_PARTIAL>, dim3(parts * splits),
+    hipLaunchKernelGGL(hk_gemm_mfma<HK_EPI_PARTIAL>, dim3(parts * splits),
                        dim3(HK_GEMM_THREADS), HK_GEMM_LDS, gpu->stream, g);
     hipLaunchKernelGGL(hk_splitk_reduce<HK_EPI_STORE>, dim3(parts * 64),
                        dim3(256), 0, gpu->stream, g, splits);

@@ -6,8 +6,8 @@ changes around the loop (an extra live value, a divergent branch in the
 tile loop) have made the register allocator rotate those blocks through
 `v_accvgpr_mov` / `v_accvgpr_write` copies inside the K loop, or spill into
 scratch there, which cost the split-K instances 60-150% of their time with
-correct results.  The 16x16x32 instances keep two L2 prefetch loads in
-flight across the stage wait; a vmcnt(0) there (which the compiler adds
+correct results.  Every instance keeps two L2 prefetch loads in flight
+across the stage wait; a vmcnt(0) there (which the compiler adds
 for a barrier with a fence) quietly cancels the prefetch, and the cold-
 weight launches of the forward lose 4-10%.  This test compiles
 csrc/hk_gemm.hip as the Makefile does
@@ -33,9 +33,9 @@ INSTANCES = {
     "hk_gemm_mfma<1> (SwiGLU)": "_Z12hk_gemm_mfmaILi1ELb0EEv12hk_gemm_args",
     "hk_gemm_mfma<2> (GELU)": "_Z12hk_gemm_mfmaILi2ELb0EEv12hk_gemm_args",
     "hk_gemm_mfma<0, group>": "_Z12hk_gemm_mfmaILi0ELb1EEv12hk_gemm_args",
-    "hk_gemm_mfma32<3> (split-K)": "_Z14hk_gemm_mfma32ILi3ELb0EEv12hk_gemm_args",
-    "hk_gemm_mfma32<4> (split-K SwiGLU)":
-        "_Z14hk_gemm_mfma32ILi4ELb0EEv12hk_gemm_args",
+    "hk_gemm_mfma<3> (split-K)": "_Z12hk_gemm_mfmaILi3ELb0EEv12hk_gemm_args",
+    "hk_gemm_mfma<4> (split-K SwiGLU)":
+        "_Z12hk_gemm_mfmaILi4ELb0EEv12hk_gemm_args",
 }
 BAD = re.compile(r"\b(v_accvgpr_mov_b32|v_accvgpr_write_b32|scratch_\w+)\b")
 
@@ -62,15 +62,19 @@ def _k_loop_offenders(extra):
         assert len(mfma) == 128, (name, len(mfma))
         loop = body[mfma[0]:mfma[-1]]
         found[name] = [l.strip() for l in loop if BAD.search(l)]
-        if "mfma32" not in sym:
-            waits = [int(m.group(1)) for l in loop
-                     for m in [re.search(r"s_waitcnt\b.*vmcnt\((\d+)\)", l)]
-                     if m]
-            pf = [l for l in loop if re.search(r"buffer_load_dword\b.*\blds\b", l)]
-            if waits != [2]:
-                found[name].append(f"stage waits vmcnt{waits}, want [2]")
-            if len(pf) != 2:
-                found[name].append(f"{len(pf)} prefetch loads, want 2")
+        waits = [int(m.group(1)) for l in loop
+                 for m in [re.search(r"s_waitcnt\b.*vmcnt\((\d+)\)", l)]
+                 if m]
+        # the prefetch loads may follow the last MFMA: count them up to the
+        # loop's back-edge branch
+        back = next(i for i in range(mfma[-1], len(body))
+                    if body[i].strip().startswith("s_cbranch"))
+        pf = [l for l in body[mfma[0]:back]
+              if re.search(r"buffer_load_dword\b.*\blds\b", l)]
+        if waits != [2]:
+            found[name].append(f"stage waits vmcnt{waits}, want [2]")
+        if len(pf) != 2:
+            found[name].append(f"{len(pf)} prefetch loads, want 2")
     return found
 
 
