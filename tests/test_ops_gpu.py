@@ -96,6 +96,8 @@ def test_linear_repeats_bit_exactly(gpu, m, k, n, bias, mlp):
     (600, 1088, 256, False),    # split-K with a short last split (17 steps)
     (4096, 512, 4352, True),    # 272 tiles: one full round + a split tail
     (4100, 256, 4200, True),    # 289 tiles, full round with ragged M and N
+    (300, 64, 520, True),       # one K stage: loads and prefetch clamp to it
+    (2378, 128, 1000, False),   # two K stages, H3 rows, ragged N
 ])
 def test_linear_bf16(gpu, m, k, n, bias):
     rng = np.random.default_rng(m * 7 + k + n)
