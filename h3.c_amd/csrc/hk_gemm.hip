@@ -26,7 +26,8 @@
  *     distinct banks;
  *   - the MFMA computes D = W_tile . X_tile^T, so each lane's accumulator
  *     holds 4 consecutive output columns of one output row: the epilogue
- *     writes 8-byte packed bf16 groups;
+ *     packs them into 8-byte bf16 groups in LDS and stores the tile as
+ *     whole rows, 16 bytes per lane;
  *   - the workgroup -> tile order is XCD-aware: consecutive workgroups are
  *     dealt round-robin to the 8 XCDs, so workgroup ids are first regrouped
  *     per XCD and then walked in GROUP_M-tall column bands, keeping the
@@ -35,7 +36,9 @@
  * Epilogues: plain store (+bias), SwiGLU (the tile's W rows interleave 64
  * gate and 64 up rows per wave so each lane holds matching gate/up values;
  * activation bf16(silu(bf16 g) * bf16 u), the reference's rounding,
- * h3_cuda_core.cu:104-114 fed by a bf16 fc1 output, :1067-1104), GELU-tanh.
+ * h3_cuda_core.cu:104-114 fed by a bf16 fc1 output, :1067-1104), GELU-tanh,
+ * and the split-K pieces' F32 partial tiles, which hk_splitk_reduce sums
+ * before the bias and activation.
  *
  * A sequential-k reference kernel (one thread per output, fmaf from the
  * bias, bf16 inputs: the reference's hand kernel h3_cuda_core.cu:358-371)
