@@ -3,8 +3,10 @@ back for a few seconds: the MFMA-only loop (h3_hip_mfma_loop), the Wan QKV
 GEMM (6144 x 5120 -> 15360, bias) and 6144-row self-attention (40 heads x
 128).  `amd-smi metric -p -c` is sampled every 0.3 s from a second thread;
 the first two and the last sample of each kernel are dropped (ramp).
+With --cold the GEMM cycles through copies of X and W larger than the
+256 MB Infinity Cache, as the forward reads every block's own weights.
 
-    python3 h3.c_amd/power_sample.py
+    python3 h3.c_amd/power_sample.py [--cold]
 """
 import csv
 import ctypes as C
@@ -25,7 +27,7 @@ def amd_smi():
                           timeout=10).stdout
 
 
-def run_for(gpu, label, launch, flops, seconds=4.0):
+def run_for(gpu, label, launch, flops, seconds=4.0, batch=20):
     samples, stop = [], threading.Event()
 
     def sampler():
@@ -37,34 +39,49 @@ def run_for(gpu, label, launch, flops, seconds=4.0):
     t0, n = time.time(), 0
     while time.time() - t0 < seconds:
         gpu.begin()
-        for _ in range(20):
+        for _ in range(batch):
             gpu.check(launch(), label)
         gpu.submit()
-        n += 20
+        n += batch
     stop.set()
     th.join()
     dt = time.time() - t0
     print(f"== {label}: {n} launches in {dt:.2f} s, {dt / n * 1e6:.1f} us "
           f"each, {flops * n / dt / 1e12:.0f} TFLOP/s", flush=True)
+    watts = []
     for out in samples[2:-1]:
         r = next(csv.DictReader(io.StringIO(out)), {})
         clk = [r.get(f"gfx_{i}_clk") for i in range(8)]
         print(f"  socket power {r.get('socket_power')} W, XCD clocks (MHz) "
               f"{' '.join(str(c) for c in clk)}", flush=True)
+        try:
+            watts.append(float(r.get("socket_power")))
+        except (TypeError, ValueError):
+            pass
+    if watts:
+        w = sum(watts) / len(watts)
+        print(f"  mean {w:.0f} W: {w * dt / n:.3f} J per launch, "
+              f"{w / (flops * n / dt) * 1e12:.2f} pJ per flop", flush=True)
 
 
 def main():
+    cold = "--cold" in sys.argv[1:]
     gpu = h3hip.Gpu()
     L = gpu.L
     try:
         m, k, n = 6144, 5120, 15360
-        x, w = gpu.new_bf16(m * k), gpu.new_bf16(n * k)
+        copies = 4 if cold else 1   # 4 x 220 MB of X and W
+        xs = [gpu.new_bf16(m * k) for _ in range(copies)]
+        ws = [gpu.new_bf16(n * k) for _ in range(copies)]
         o, b = gpu.new_bf16(m * n), gpu.new_bf16(n)
         rows, heads = 6144, 40
         q, kk, v, oo = (gpu.new_bf16(rows * heads * 128) for _ in range(4))
         gpu.begin()
-        L.h3_gpu_fill_normal_bf16(gpu.h, x, 0, m * k, 1, 0.0, 1.0)
-        L.h3_gpu_fill_normal_bf16(gpu.h, w, 0, n * k, 2, 0.0, 0.02)
+        for i in range(copies):
+            L.h3_gpu_fill_normal_bf16(gpu.h, xs[i], 0, m * k, 1 + 10 * i,
+                                      0.0, 1.0)
+            L.h3_gpu_fill_normal_bf16(gpu.h, ws[i], 0, n * k, 2 + 10 * i,
+                                      0.0, 0.02)
         L.h3_gpu_fill_normal_bf16(gpu.h, b, 0, n, 3, 0.0, 0.02)
         for t, seed in ((q, 5), (kk, 6), (v, 7)):
             L.h3_gpu_fill_normal_bf16(gpu.h, t, 0, rows * heads * 128, seed,
@@ -80,9 +97,15 @@ def main():
         run_for(gpu, "MFMA-only loop (h3_hip_mfma_loop)",
                 lambda: L.h3_hip_mfma_loop(gpu.h, sink, 20000, C.byref(fl)),
                 per_iteration * 20000)
-        run_for(gpu, "QKV GEMM 6144x5120->15360 (hk_gemm_mfma<0>)",
-                lambda: L.h3_gpu_linear_bf16(gpu.h, o, x, w, b, m, k, n),
-                2.0 * m * n * k)
+        turn = [0]
+
+        def gemm():
+            i = turn[0] % copies
+            turn[0] += 1
+            return L.h3_gpu_linear_bf16(gpu.h, o, xs[i], ws[i], b, m, k, n)
+        run_for(gpu, "QKV GEMM 6144x5120->15360 (hk_gemm_mfma<0>)"
+                + (f", X and W cycling over {copies} copies" if cold else ""),
+                gemm, 2.0 * m * n * k)
         run_for(gpu, "self-attention 6144 rows, 40 heads (hk_flash_fwd)",
                 lambda: L.h3_gpu_sdpa_bf16(gpu.h, oo, q, kk, v, rows, heads,
                                            128, C.c_float(128 ** -0.5)),
